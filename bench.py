@@ -1,0 +1,310 @@
+#!/usr/bin/env python3
+"""Benchmark of the fused dequant + decode-attention path on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--L 16384] [--G 32]
+
+One "step" is one decode step: one query token attending over L cached
+positions for all H=32 heads (D=128), i.e. one va_decode() call (split-L
+attention pass + log-sum-exp merge pass), reading a compressed K/V cache that is
+already resident in HBM. The headline workload is BASELINE.json's metric at
+H=32 D=128 L=16384 with G=32 scales; `value` is the q8+ (fused INT8) decode
+rate in tok/s. f16, f16+ and q4+ at the same shape are reported in
+`formats`, each with ms, GB/s, MBU against the probed read ceiling, % of the
+8 TB/s peak, and tok/s.
+
+Method (reference bench, src/voltattn.cu:967-1070, re-derived for MI355X):
+  * read ceiling: a >= 4 GiB buffer (16x the 256 MB Infinity Cache) read with
+    128-bit loads, best over launch shapes (va_probe_read);
+  * K/V are drawn N(0,1) on the GPU, quantized there (bit-exact quantizer) and
+    replicated into enough copies to rotate a >= 2 GiB working set, so the
+    MALL cannot serve the stream;
+  * timed region: K back-to-back steps between two HIP events on the launch
+    stream, bracketed by device synchronisation -> ms_per_step (the value);
+    plus the reference's best-of-K single-launch time, each launch preceded by
+    an untimed one so the start event is stamped when the GPU is already busy;
+  * roofline: algorithmic bytes per decode-kernel launch (compressed K+V
+    payload + fp16 scales: 2*H*L*(D*b/8 + 2*D/G)) over the decode kernel's
+    mean launch time (K back-to-back first-pass launches between events);
+  * cpu_baseline: the oracle's double-precision reference attention
+    (reference(), src/voltattn.cu:769-794) over the same shape, timed on this
+    host (rank 0, N=1 only).
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+METRIC = "tok/s + %MBU vs probed HBM ceiling, f16/q8+/q4+ at H32 D128 L16K"
+PEAK_HBM_GBPS = 8000.0
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def algo_bytes(fmt, H, L, D, G) -> int:
+    import voltattn_amd as va
+    return 2 * (va.payload_bytes(fmt, H, L, D) + va.scale_bytes(fmt, H, L, D, G))
+
+
+class Workload:
+    """Rotated copies of one format's K/V cache (+ scales) resident in HBM."""
+
+    def __init__(self, va, fmt, H, L, D, G, min_set_bytes, max_copies, seed=0x1234):
+        self.va, self.fmt, self.H, self.L, self.D, self.G = va, fmt, H, L, D, G
+        n = H * L * D
+        self.pay = va.payload_bytes(fmt, H, L, D)
+        self.sc = va.scale_bytes(fmt, H, L, D, G)
+        self.copy_bytes = 2 * (self.pay + self.sc)
+        self.copies = max(1, min(max_copies, math.ceil(min_set_bytes / self.copy_bytes)))
+        al = lambda x: (x + 4095) // 4096 * 4096
+        self.pay_al, self.sc_al = al(self.pay), al(max(self.sc, 1))
+        self.bufs = []
+        self.K = self._alloc(self.pay_al * self.copies)
+        self.V = self._alloc(self.pay_al * self.copies)
+        self.SK = self._alloc(self.sc_al * self.copies) if self.sc else None
+        self.SV = self._alloc(self.sc_al * self.copies) if self.sc else None
+        self.q = self._alloc(H * D * 2)
+        self.out = self._alloc(H * D * 2)
+        # copy 0 from seeded N(0,1) draws, on the device
+        x = va.DeviceBuffer(n * 4)
+        try:
+            bits = va.fmt_bits(fmt)
+            for dst, sdst, s in ((self.K, self.SK, seed), (self.V, self.SV, seed + 0x4444)):
+                va.fill_normal(x.ptr, n, s)
+                if bits == 16:
+                    va.f32_to_f16(x.ptr, n, dst.ptr)
+                else:
+                    va.quantize(bits, G, x.ptr, H * L, D, dst.ptr, sdst.ptr)
+            va.fill_normal(x.ptr, H * D, seed + 0x8888)
+            va.f32_to_f16(x.ptr, H * D, self.q.ptr)
+            va.sync()
+        finally:
+            x.free()
+        for c in range(1, self.copies):
+            va.check(va.lib.va_memcpy_d2d(self.K.ptr + c * self.pay_al, self.K.ptr, self.pay, None))
+            va.check(va.lib.va_memcpy_d2d(self.V.ptr + c * self.pay_al, self.V.ptr, self.pay, None))
+            if self.sc:
+                va.check(va.lib.va_memcpy_d2d(self.SK.ptr + c * self.sc_al, self.SK.ptr, self.sc, None))
+                va.check(va.lib.va_memcpy_d2d(self.SV.ptr + c * self.sc_al, self.SV.ptr, self.sc, None))
+        va.sync()
+        self.ws = None
+        self.S = None
+
+    def _alloc(self, nbytes):
+        b = self.va.DeviceBuffer(nbytes)
+        self.bufs.append(b)
+        return b
+
+    def set_splits(self, S):
+        if self.ws is not None:
+            self.ws.free()
+            self.bufs.remove(self.ws)
+        self.S = S
+        self.ws = self._alloc(self.va.ws_bytes(self.H, self.D, S))
+
+    def bufs_for(self, c):
+        va = self.va
+        return va.DeviceBufs(K=self.K.ptr + c * self.pay_al, V=self.V.ptr + c * self.pay_al,
+                             scK=self.SK.ptr + c * self.sc_al if self.sc else 0,
+                             scV=self.SV.ptr + c * self.sc_al if self.sc else 0,
+                             q=self.q.ptr, out=self.out.ptr, ws=self.ws.ptr)
+
+    def free(self):
+        for b in self.bufs:
+            b.free()
+        self.bufs = []
+
+
+def time_workload(va, w: Workload, steps: int, warmup: int, stream) -> dict:
+    H, L, D, G, S, fmt = w.H, w.L, w.D, w.G, w.S, w.fmt
+    bufs = [w.bufs_for(c) for c in range(w.copies)]
+    launch = lambda c: va.launch(fmt, bufs[c % w.copies], H, L, D, S, G=G, stream=stream)
+    first = lambda c: va.decode_splits(fmt, bufs[c % w.copies], H, L, D, S, G=G, stream=stream)
+    e0, e1 = va.Event(), va.Event()
+    try:
+        for i in range(warmup):
+            launch(i)
+        va.sync()
+        # (1) K back-to-back steps, rotating copies: the contract's timed region
+        va.sync()
+        e0.record(stream)
+        for i in range(steps):
+            launch(i)
+        e1.record(stream)
+        e1.synchronize()
+        va.sync()
+        mean_ms = e0.elapsed_ms(e1) / steps
+        # (2) reference method: best single launch, each behind an untimed lead launch
+        best_ms = float("inf")
+        for i in range(steps):
+            launch(2 * i + 1)
+            e0.record(stream)
+            launch(2 * i + 2)
+            e1.record(stream)
+            e1.synchronize()
+            best_ms = min(best_ms, e0.elapsed_ms(e1))
+        # (3) first pass alone, back-to-back: the decode kernel's mean launch time
+        e0.record(stream)
+        for i in range(steps):
+            first(i)
+        e1.record(stream)
+        e1.synchronize()
+        kern_ms = e0.elapsed_ms(e1) / steps
+    finally:
+        e0.destroy()
+        e1.destroy()
+    return {"mean_ms": mean_ms, "best_ms": best_ms, "kernel_ms": kern_ms}
+
+
+def cpu_baseline(H, L, D, G) -> dict:
+    """The oracle's reference() on one full decode step of the workload (q8 inputs)."""
+    import numpy as np
+    import oracle
+    t0 = time.time()
+    c = oracle.make_case(8, H, L, D, G, 0x1234 + L)
+    prep_s = time.time() - t0
+    kd, vd, q = c["kd"], c["vd"], c["q"]
+    best = float("inf")
+    for _ in range(3):
+        t = time.perf_counter()
+        out = oracle.reference(kd, vd, q, H, L, D)
+        best = min(best, time.perf_counter() - t)
+    threads = max(1, min(H, 16, os.cpu_count() or 1))
+    best_mt = float("inf")
+    for _ in range(3):
+        t = time.perf_counter()
+        out_mt = oracle.reference(kd, vd, q, H, L, D, threads=threads)
+        best_mt = min(best_mt, time.perf_counter() - t)
+    assert np.array_equal(out, out_mt)
+    return {
+        "value": 1.0 / best, "unit": "tok/s", "cores": 1, "kind": "port",
+        "sample": (f"one full decode step (q8, H={H} D={D} L={L} G={G}): double-precision "
+                   f"reference() over the dequantized K/V, best of 3 single-thread runs"),
+        "ms": best * 1e3,
+        "multithread": {"value": 1.0 / best_mt, "unit": "tok/s", "cores": threads,
+                        "ms": best_mt * 1e3},
+        "input_prep_s": prep_s,
+    }
+
+
+def load_traffic(name: str):
+    p = ROOT / "profiles" / "traffic.json"
+    if p.exists():
+        try:
+            return json.loads(p.read_text()).get(name)
+        except (ValueError, OSError):
+            return None
+    return None
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--L", type=int, default=16384)
+    ap.add_argument("--G", type=int, default=32)
+    ap.add_argument("--H", type=int, default=32)
+    ap.add_argument("--D", type=int, default=128)
+    ap.add_argument("--formats", default="f16,f16+,q8+,q4+")
+    ap.add_argument("--headline", default="q8+")
+    ap.add_argument("--splits", type=int, default=0, help="force S (0: va_pick_splits)")
+    ap.add_argument("--probe-gib", type=float, default=4.0)
+    ap.add_argument("--set-gib", type=float, default=2.0, help="rotated working set per format")
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args()
+
+    if args.gpus != 1:
+        log(f"bench.py: --gpus {args.gpus} is not supported: this build runs on one MI355X; "
+            f"the path shards by heads or by L (see DESIGN.md), run with --gpus 1")
+        return 2
+    if args.steps < 1:
+        log("bench.py: --steps must be >= 1")
+        return 2
+
+    import voltattn_amd as va
+    info = va.device_info()
+    log(f"device: {info['name']} {info['arch']} CUs={info['compute_units']} "
+        f"mem={info['total_mem'] / 2**30:.0f} GiB")
+    ceiling = va.probe_read(int(args.probe_gib * 2**30), reps=5)
+    log(f"probed read ceiling: {ceiling:.1f} GB/s ({args.probe_gib:g} GiB buffer)")
+
+    H, L, D, G = args.H, args.L, args.D, args.G
+    stream = va.Stream()
+    rows = {}
+    for name in [s for s in args.formats.split(",") if s]:
+        fmt = va.Fmt.parse(name)
+        w = Workload(va, fmt, H, L, D, G, int(args.set_gib * 2**30), 256)
+        try:
+            S = args.splits or va.pick_splits(fmt, H, L, D)
+            w.set_splits(S)
+            t = time_workload(va, w, args.steps, args.warmup, stream)
+        finally:
+            w.free()
+        nbytes = algo_bytes(fmt, H, L, D, G)
+        gbs = nbytes / (t["mean_ms"] * 1e6)
+        rows[fmt.label] = {
+            "ms": t["mean_ms"], "best_single_ms": t["best_ms"], "kernel_ms": t["kernel_ms"],
+            "tok_s": 1e3 / t["mean_ms"], "tok_s_best_single": 1e3 / t["best_ms"],
+            "bytes": nbytes, "gbps": gbs, "mbu": gbs / ceiling, "pct_peak": gbs / PEAK_HBM_GBPS,
+            "kernel_gbps": nbytes / (t["kernel_ms"] * 1e6),
+            "S": S, "copies": w.copies, "working_set_bytes": w.copies * w.copy_bytes,
+        }
+        r = rows[fmt.label]
+        log(f"{fmt.label:5s} L={L} G={G} S={S:3d} copies={w.copies:3d}  "
+            f"mean {r['ms'] * 1e3:8.2f} us  best {r['best_single_ms'] * 1e3:8.2f} us  "
+            f"kernel {r['kernel_ms'] * 1e3:8.2f} us  {gbs:7.1f} GB/s  MBU {100 * r['mbu']:5.1f}%  "
+            f"tok/s {r['tok_s']:8.0f}")
+    stream.destroy()
+    for r in rows.values():
+        if "f16" in rows:
+            r["vs_f16"] = rows["f16"]["ms"] / r["ms"]
+        if "f16+" in rows:
+            r["vs_f16p"] = rows["f16+"]["ms"] / r["ms"]
+
+    head = rows[args.headline]
+    kern_gbs = head["kernel_gbps"]
+    roofline = {"bound": "hbm", "achieved": kern_gbs, "peak": PEAK_HBM_GBPS, "unit": "GB/s",
+                "frac": kern_gbs / PEAK_HBM_GBPS, "traffic": load_traffic(f"{args.headline}_L{L}_G{G}"),
+                "kernel": f"decode_tiled<{args.headline}> (first pass)",
+                "algorithmic_bytes_per_launch": head["bytes"],
+                "kernel_ms": head["kernel_ms"], "frac_of_probed": kern_gbs / ceiling}
+    cpu = None
+    if not args.no_cpu:
+        cpu = cpu_baseline(H, L, D, G)
+        log(f"cpu baseline: {cpu['value']:.3f} tok/s single-thread ({cpu['ms']:.0f} ms), "
+            f"{cpu['multithread']['value']:.2f} tok/s on {cpu['multithread']['cores']} threads")
+
+    line = {
+        "metric": METRIC, "value": head["tok_s"], "unit": "tok/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": head["ms"],
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "fp32", "data": "synthetic",
+        "config": {"workload": f"{args.headline} decode step, batch 1, H={H} D={D} L={L} G={G} "
+                               f"(BASELINE configs[1]-[3] shape)",
+                   "H": H, "D": D, "L": L, "G": G, "S": head["S"], "copies": head["copies"],
+                   "storage": {"f16": "fp16", "f16+": "fp16", "q8": "int8", "q8+": "int8",
+                               "q4": "int4", "q4+": "int4", "q3+": "int3"}[args.headline],
+                   "parallelism": "single GPU, split-L"},
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+        "probed_ceiling_gbps": ceiling,
+        "mbu": head["mbu"],
+        "formats": rows,
+        "device": info["name"], "compute_units": info["compute_units"],
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

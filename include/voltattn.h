@@ -1,0 +1,182 @@
+/* voltattn.h — C ABI of the MI355X (gfx950) fused dequant + decode-attention
+ * library libvoltattn_hip.so.
+ *
+ * The reference (kamilch1k/voltattn) has no plugin or FFI layer: its path sits
+ * behind the file-static C++ function
+ *     void launch(Fmt f, const DeviceBufs& b, int H, int L, int D, int S)
+ * (src/voltattn.cu:803-835), fed by host-side format code and a CUDA runtime
+ * used directly. This header is that boundary as a C ABI: plain pointers,
+ * sizes and int status codes, no HIP or torch types. Every entry point names
+ * the reference interface it replaces.
+ *
+ * Conventions
+ *   - Every function returns VA_OK (0) or a VA_E* code; va_last_error() gives
+ *     the calling thread's message for the last failure.
+ *   - "Device pointer" means memory from va_malloc (or any HIP device
+ *     allocation). The caller owns every buffer, as in the reference.
+ *   - `stream` is a hipStream_t passed as void*; NULL is the default stream.
+ *     Launch functions are asynchronous, like the reference's launch().
+ *   - Layouts (src/voltattn.cu:92-93, 676-745):
+ *       K, V payload  [H][L][row]  row = 2*D bytes (f16), D (q8), D/2 (q4), 3*D/8 (q3)
+ *         q8: int8 per element; q4: element e in byte e/2, low nibble first,
+ *         stored v+8; q3: element e at bits [3e, 3e+3) of a little-endian
+ *         stream (8 elements per 3-byte granule), stored v+4;
+ *       scales        [H][L][D/G]  fp16 bits (quantized formats only)
+ *       q, out        [H][D]       fp16 bits
+ *       ws            va_ws_bytes(H, D, S) bytes; fully overwritten each call.
+ */
+#ifndef VOLTATTN_H
+#define VOLTATTN_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define VA_ABI_VERSION 1
+
+/* Status codes. */
+enum {
+    VA_OK       = 0,
+    VA_EINVAL   = 1,  /* bad argument: format, shape, group size, split count */
+    VA_EALIGN   = 2,  /* pointer alignment the kernels require is not met */
+    VA_ENULL    = 3,  /* a required pointer is NULL */
+    VA_ERANGE   = 4,  /* shape exceeds the 32-bit buffer addressing of a head */
+    VA_EHIP     = 5,  /* HIP runtime or launch error */
+    VA_ENODEV   = 6   /* no usable gfx950 device */
+};
+
+/* Formats: the reference's enum class Fmt {F16, F16M, Q8, Q8M, Q4, Q4M, Q3M}
+ * (src/voltattn.cu:676). The "+" formats select the tiled multi-position
+ * kernels; the others the naive one-position-per-wave kernels. */
+typedef enum {
+    VA_F16  = 0,   /* f16   naive  (attn_f16,     src/voltattn.cu:122-187) */
+    VA_F16P = 1,   /* f16+  tiled  (attn_f16_mlp, src/voltattn.cu:364-423) */
+    VA_Q8   = 2,   /* q8    naive  (attn_q8,      src/voltattn.cu:189-252) */
+    VA_Q8P  = 3,   /* q8+   tiled  (attn_q8_mlp,  src/voltattn.cu:425-490) */
+    VA_Q4   = 4,   /* q4    naive  (attn_q4,      src/voltattn.cu:254-320) */
+    VA_Q4P  = 5,   /* q4+   tiled  (attn_q4_mlp,  src/voltattn.cu:492-561) */
+    VA_Q3P  = 6    /* q3+   tiled  (attn_q3_mlp,  src/voltattn.cu:563-649) */
+} va_fmt;
+
+/* Device buffers of one decode step: the reference's struct DeviceBufs
+ * {K, V, scK, scV, q, out, ws} (src/voltattn.cu:796-801).
+ * Alignment: k, v 16 bytes (4 for q3); sk, sv 4 bytes (2 when D/G == 1);
+ * q 16 bytes; out 2 bytes; ws 4 bytes. sk/sv are ignored for f16 formats. */
+typedef struct {
+    const void*     k;
+    const void*     v;
+    const uint16_t* sk;
+    const uint16_t* sv;
+    const uint16_t* q;
+    uint16_t*       out;
+    float*          ws;
+} va_bufs;
+
+/* One decode step: per head softmax(q.K^T / sqrt(D)) V over L positions,
+ * split into S chunks of ceil(L/S) positions, partials merged by log-sum-exp,
+ * fp16 output. Replaces launch() (src/voltattn.cu:803-835), adding the group
+ * size G (the reference fixes GROUP = 64, src/voltattn.cu:60).
+ * Valid: D in {64,128}; G in {32,64} with G <= D (ignored for f16 formats);
+ * H >= 1; L >= 1; S >= 1. Asynchronous on `stream`. */
+int va_decode(va_fmt fmt, const va_bufs* b, int H, int L, int D, int G, int S, void* stream);
+
+/* First pass only: writes the S partials (m, l, o[D]) per head into b->ws
+ * (the attention kernels of launch(), src/voltattn.cu:813-833). `out` unused. */
+int va_decode_splits(va_fmt fmt, const va_bufs* b, int H, int L, int D, int G, int S,
+                     void* stream);
+
+/* Second pass only: log-sum-exp merge of S partials per head into fp16 out
+ * (combine, src/voltattn.cu:651-672). */
+int va_merge(const float* ws, uint16_t* out, int H, int D, int S, void* stream);
+
+/* Workspace bytes for (H, D, S): H*S*(D+2) floats, the reference's
+ * cudaMalloc(&b.ws, H*S*(D+2)*4) (src/voltattn.cu:888). */
+size_t va_ws_bytes(int H, int D, int S);
+
+/* Payload bytes of K (or V) for a format: the reference's qbytes() / n*2
+ * (src/voltattn.cu:692, 990-991). 0 for an invalid format. */
+size_t va_payload_bytes(va_fmt fmt, int H, int L, int D);
+
+/* Scale bytes of K (or V): H*L*(D/G)*2, 0 for f16 formats
+ * (src/voltattn.cu:880-881, 991). */
+size_t va_scale_bytes(va_fmt fmt, int H, int L, int D, int G);
+
+/* Positions per split the library would use for (L, S): ceil(L/S), the
+ * reference's chunk (src/voltattn.cu:804). */
+int va_split_chunk(int L, int S);
+
+/* A split count that fills the device for (fmt, H, L, D): the reference's
+ * S = max(1, min(2*SMs/H, ceil(L/512))) (src/voltattn.cu:1026) re-derived
+ * for 256 CUs and the tiled kernels' work-group tile. */
+int va_pick_splits(va_fmt fmt, int H, int L, int D, int* S);
+
+/* Printable format name, "f16", "f16+", ... (fmt_name, src/voltattn.cu:677-687). */
+const char* va_fmt_name(va_fmt fmt);
+
+/* Device-side symmetric per-group quantizer + packer, bit-exact with the
+ * reference's host quantize() (src/voltattn.cu:705-745) for G in {32,64}.
+ * x: device fp32 [rows][D]; packed: rows*D*bits/8 bytes (4-byte aligned);
+ * scales: rows*(D/G) fp16. bits in {8,4,3}. */
+int va_quantize(int bits, int G, const float* x, size_t rows, int D, void* packed,
+                uint16_t* scales, void* stream);
+
+/* Device-side fp32 -> fp16 round-to-nearest-even over n values (the
+ * reference's __float2half loops, src/voltattn.cu:866-868, 1000-1002). */
+int va_f32_to_f16(const float* x, size_t n, uint16_t* out, void* stream);
+
+/* Seeded N(0,1) fill of n fp32 values on the device (bench data; the
+ * reference's fill_fast, src/voltattn.cu:959-965, fills on the host). */
+int va_fill_normal(float* x, size_t n, uint64_t seed, void* stream);
+
+/* Empirical HBM read ceiling: best GB/s over `reps` timed reads of a
+ * `bytes`-sized device buffer, taking the best of several launch shapes
+ * (probe_ceiling + read_kernel, src/voltattn.cu:64-78, 935-957). */
+int va_probe_read(size_t bytes, int reps, double* best_gbps);
+
+/* ---- runtime shims (the reference calls the CUDA runtime directly:
+ *      cudaMalloc/cudaMemcpy/cudaFree/cudaEvent*, src/voltattn.cu:863-895, 936-955,
+ *      cudaGetDeviceProperties, src/voltattn.cu:968-971) ---- */
+typedef struct {
+    char   name[256];
+    char   arch[64];          /* e.g. "gfx950:sramecc+:xnack-" */
+    int    compute_units;
+    int    clock_khz;
+    int    mem_clock_khz;
+    int    mem_bus_bits;
+    size_t total_mem;
+    size_t l2_bytes;
+} va_device_info_t;
+
+int va_device_count(int* n);
+int va_set_device(int dev);
+int va_device_info(va_device_info_t* info);
+int va_malloc(void** p, size_t bytes);
+int va_free(void* p);
+int va_memcpy_h2d(void* dst, const void* src, size_t bytes);
+int va_memcpy_d2h(void* dst, const void* src, size_t bytes);
+int va_memcpy_d2d(void* dst, const void* src, size_t bytes, void* stream);
+int va_memset(void* p, int value, size_t bytes);
+int va_sync(void);
+int va_stream_create(void** stream);
+int va_stream_destroy(void* stream);
+int va_stream_sync(void* stream);
+int va_event_create(void** ev);
+int va_event_destroy(void* ev);
+int va_event_record(void* ev, void* stream);
+int va_event_sync(void* ev);
+int va_event_elapsed_ms(void* start, void* stop, float* ms);
+
+/* Message of the calling thread's last failure ("" if none). */
+const char* va_last_error(void);
+
+/* VA_ABI_VERSION of the loaded library. */
+int va_abi_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* VOLTATTN_H */

@@ -1,0 +1,106 @@
+"""Build recipe for the in-tree native artefacts.
+
+    python -m voltattn_amd.build            # library + oracle + CLI harness
+
+* ``voltattn_amd/libvoltattn_hip.so`` — the product: gfx950 HIP kernels and the
+  C ABI of ``include/voltattn.h`` (hipcc, one object per ``csrc/*.hip``).
+* ``oracle/liboracle.so`` — the CPU checker (test infrastructure, g++).
+* ``build/voltattn`` — the C++ selftest/bench/probe harness (tests/cli), linked
+  against both.
+
+Everything is compiled every time (the driver's "does it build" check); objects
+go to ``build/obj`` and the shared library is replaced atomically.
+"""
+from __future__ import annotations
+
+import concurrent.futures as cf
+import os
+import shutil
+import subprocess
+import sys
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent.parent
+PKG = ROOT / "voltattn_amd"
+CSRC = PKG / "csrc"
+OBJ = ROOT / "build" / "obj"
+LIB = PKG / "libvoltattn_hip.so"
+ARCH = "gfx950"
+
+HIPCC_FLAGS = [
+    f"--offload-arch={ARCH}",
+    "-O3",
+    "-std=c++17",
+    "-fPIC",
+    "-Wall",
+    "-Wextra",
+    "-Werror",
+    "-Wno-unused-command-line-argument",
+    # Keep hipcc from forming packed-FP32 (v_pk_*_f32) instructions.
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+]
+
+
+def hipcc() -> str:
+    for cand in (os.environ.get("HIPCC"), "/opt/rocm/bin/hipcc", shutil.which("hipcc")):
+        if cand and Path(cand).exists():
+            return cand
+    raise RuntimeError("hipcc not found (ROCm is required to build voltattn_amd)")
+
+
+def _run(cmd: list[str], cwd: Path | None = None) -> None:
+    res = subprocess.run(cmd, cwd=cwd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"command failed ({res.returncode}): {' '.join(cmd)}\n{res.stdout}\n{res.stderr}")
+
+
+def build_library(jobs: int = 8) -> Path:
+    OBJ.mkdir(parents=True, exist_ok=True)
+    srcs = sorted(CSRC.glob("*.hip"))
+    cc = hipcc()
+
+    def compile_one(src: Path) -> Path:
+        obj = OBJ / (src.stem + ".o")
+        _run([cc, *HIPCC_FLAGS, "-I", str(ROOT / "include"), "-c", str(src), "-o", str(obj)])
+        return obj
+
+    with cf.ThreadPoolExecutor(max_workers=max(1, jobs)) as ex:
+        objs = list(ex.map(compile_one, srcs))
+    tmp = LIB.with_suffix(".so.tmp")
+    _run([cc, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *map(str, objs)])
+    os.replace(tmp, LIB)
+    return LIB
+
+
+def build_oracle() -> Path:
+    _run(["make", "-s", "-C", str(ROOT / "oracle")])
+    return ROOT / "oracle" / "liboracle.so"
+
+
+def build_cli() -> Path:
+    out = ROOT / "build" / "voltattn"
+    out.parent.mkdir(parents=True, exist_ok=True)
+    tmp = out.with_name("voltattn.tmp")
+    _run([
+        "g++", "-O2", "-std=c++17", "-Wall", "-Wextra", "-Werror", "-pthread",
+        "-I", str(ROOT / "include"), "-I", str(ROOT / "oracle"),
+        str(ROOT / "tests" / "cli" / "voltattn_cli.cpp"),
+        "-o", str(tmp),
+        f"-L{PKG}", "-lvoltattn_hip", f"-Wl,-rpath,{PKG}", f"-Wl,-rpath,$ORIGIN/../voltattn_amd",
+        f"-L{ROOT / 'oracle'}", "-loracle", f"-Wl,-rpath,{ROOT / 'oracle'}",
+        "-Wl,-rpath,$ORIGIN/../oracle",
+    ])
+    os.replace(tmp, out)
+    return out
+
+
+def build_all(jobs: int = 8) -> None:
+    build_library(jobs)
+    build_oracle()
+    if (ROOT / "tests" / "cli" / "voltattn_cli.cpp").exists():
+        build_cli()
+
+
+if __name__ == "__main__":
+    build_all(int(sys.argv[1]) if len(sys.argv) > 1 else 8)
+    print(f"built {LIB}")

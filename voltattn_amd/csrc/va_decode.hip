@@ -1,0 +1,536 @@
+// va_decode.hip — fused dequant + split-L decode attention for gfx950.
+//
+// One work-group (4 wave64) per (head h, split s) computes a log-sum-exp
+// partial (m, l, o[D]) over positions [s*chunk, min(L, (s+1)*chunk)) of head h
+// (flash-decoding; reference src/voltattn.cu:80-120, 122-649). A second pass
+// (va_merge.hip) merges the S partials of each head.
+//
+// Tiled ("+") kernels. A position row of ROWB compressed bytes is read by LP
+// lanes, each taking LB = 16 contiguous bytes (12 for q3) with one buffer
+// load, so one wave-wide load instruction covers PPW = 64/LP consecutive rows
+// (1 KiB; 768 B for q3) with no gaps. Each lane dequantizes its EPL elements in
+// registers (bit ops, one convert and one FMA per element), the partial dot is
+// summed over the LP lanes with DPP row ops, and the online softmax runs in
+// fp32 in log2 units (q is pre-scaled by log2(e)/sqrt(D), exponentials are
+// v_exp_f32). Per wave and iteration U rows per lane are in flight for K and
+// V, and the next tile is prefetched into registers while the current one is
+// computed. The fp16 group scales of a wave's tile are fetched with one
+// coalesced load per tensor and staged once in LDS as (k, v) pairs.
+//
+// The running maximum is shared by the whole wave and is raised lazily: a
+// rescale (one cross-lane max and a multiply of l and o) happens only when a
+// new score exceeds it by more than RESCALE_SLACK (log2 units), so weights
+// stay <= 2^RESCALE_SLACK and most tiles skip the rescale entirely. (o, l, m)
+// always describe the same normalised value, so the result is unchanged.
+//
+// Quantized codes are consumed unsigned (q8 xor 0x80, q4 nibble, q3 field)
+// with v_cvt_f32_ubyte; the constant code offset is removed once: from the
+// score via the lane's sum of q, and from o via the running sum of the
+// weights (E), so the inner loop has no per-element subtraction.
+//
+// Naive kernels (f16, q8, q4): one wave64 per position, D/64 elements per
+// lane, a 6-step cross-lane sum and an exact per-position online-softmax
+// update — the attribution control of the reference's attn_f16/q8/q4
+// (src/voltattn.cu:122-320).
+#include "va_device.hpp"
+#include "va_kernels.hpp"
+
+namespace va {
+
+constexpr int WAVES = 4;                 // waves per work-group
+constexpr float RESCALE_SLACK = 8.0f;    // log2 units: weights stay <= 256
+constexpr float M_INIT = -1e30f;         // finite "no score yet" maximum
+
+// --------------------------------------------------------------- layouts ----
+template <int KIND, int D> struct Tile {
+    static constexpr int ROWB = RowBytes<KIND, D>::value;   // bytes per row
+    static constexpr int LB   = KIND == KQ3 ? 12 : 16;      // bytes per lane per row
+    static constexpr int LP   = ROWB / LB;                  // lanes per row
+    static constexpr int PPW  = 64 / LP;                    // rows per wave load
+    static constexpr int EPL  = D / LP;                     // elements per lane
+    static_assert(ROWB % LB == 0 && 64 % LP == 0 && LP <= 16, "lane split");
+};
+
+// Rows per lane in flight per tile (per tensor).
+template <int KIND, int D> struct Unroll { static constexpr int value = KIND == KF16 ? 4 : 2; };
+
+template <int KIND> struct LaneLoad { using type = u32x4; };
+template <> struct LaneLoad<KQ3> { using type = u32x3; };
+
+template <int KIND>
+__device__ __forceinline__ typename LaneLoad<KIND>::type
+lane_load(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+    if constexpr (KIND == KQ3) return ld96(r, voff, soff);
+    else return ld128(r, voff, soff);
+}
+
+__device__ __forceinline__ float ubyte(uint32_t w, int b) {
+    return (float)((w >> (8 * b)) & 0xFFu);              // v_cvt_f32_ubyte{b}
+}
+
+// 3-bit field e (0..31) of a 96-bit little-endian lane word.
+__device__ __forceinline__ uint32_t field3(const u32x3& w, int e) {
+    const int b = 3 * e;
+    if (b + 3 <= 32) return (w.x >> b) & 7u;
+    if (b < 32)      return __builtin_amdgcn_alignbit(w.y, w.x, b) & 7u;
+    if (b + 3 <= 64) return (w.y >> (b - 32)) & 7u;
+    if (b < 64)      return __builtin_amdgcn_alignbit(w.z, w.y, b - 32) & 7u;
+    return (w.z >> (b - 64)) & 7u;
+}
+
+// Per-kind lane codec: dot(q, codes) and o += ev * codes over EPL elements.
+template <int KIND> struct Codec;
+
+template <> struct Codec<KF16> {                 // 8 halves per lane
+    static constexpr int EPL = 8;
+    __device__ static float dot(const u32x4& w, const float* qv) {
+        float acc = 0.f;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            acc = __builtin_fmaf(h2f_lo(w[i]), qv[2 * i], acc);
+            acc = __builtin_fmaf(h2f_hi(w[i]), qv[2 * i + 1], acc);
+        }
+        return acc;
+    }
+    __device__ static void axpy(const u32x4& w, float ev, float* o) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            o[2 * i]     = __builtin_fmaf(ev, h2f_lo(w[i]), o[2 * i]);
+            o[2 * i + 1] = __builtin_fmaf(ev, h2f_hi(w[i]), o[2 * i + 1]);
+        }
+    }
+};
+
+template <> struct Codec<KQ8> {                  // 16 int8 per lane, consumed as u8 = v + 128
+    static constexpr int EPL = 16;
+    __device__ static float dot(const u32x4& w, const float* qv) {
+        float acc = 0.f;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const uint32_t u = w[i] ^ 0x80808080u;
+#pragma unroll
+            for (int b = 0; b < 4; ++b) acc = __builtin_fmaf(ubyte(u, b), qv[4 * i + b], acc);
+        }
+        return acc;
+    }
+    __device__ static void axpy(const u32x4& w, float ev, float* o) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const uint32_t u = w[i] ^ 0x80808080u;
+#pragma unroll
+            for (int b = 0; b < 4; ++b)
+                o[4 * i + b] = __builtin_fmaf(ev, ubyte(u, b), o[4 * i + b]);
+        }
+    }
+};
+
+template <> struct Codec<KQ4> {                  // 32 nibbles per lane (v + 8), low nibble first
+    static constexpr int EPL = 32;
+    __device__ static float dot(const u32x4& w, const float* qv) {
+        float acc = 0.f;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const uint32_t lo = w[i] & 0x0F0F0F0Fu;          // elements 8i + 2b
+            const uint32_t hi = (w[i] >> 4) & 0x0F0F0F0Fu;   // elements 8i + 2b + 1
+#pragma unroll
+            for (int b = 0; b < 4; ++b) {
+                acc = __builtin_fmaf(ubyte(lo, b), qv[8 * i + 2 * b], acc);
+                acc = __builtin_fmaf(ubyte(hi, b), qv[8 * i + 2 * b + 1], acc);
+            }
+        }
+        return acc;
+    }
+    __device__ static void axpy(const u32x4& w, float ev, float* o) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const uint32_t lo = w[i] & 0x0F0F0F0Fu;
+            const uint32_t hi = (w[i] >> 4) & 0x0F0F0F0Fu;
+#pragma unroll
+            for (int b = 0; b < 4; ++b) {
+                o[8 * i + 2 * b]     = __builtin_fmaf(ev, ubyte(lo, b), o[8 * i + 2 * b]);
+                o[8 * i + 2 * b + 1] = __builtin_fmaf(ev, ubyte(hi, b), o[8 * i + 2 * b + 1]);
+            }
+        }
+    }
+};
+
+template <> struct Codec<KQ3> {                  // 32 3-bit fields per lane (v + 4)
+    static constexpr int EPL = 32;
+    __device__ static float dot(const u32x3& w, const float* qv) {
+        float acc = 0.f;
+#pragma unroll
+        for (int e = 0; e < 32; ++e) acc = __builtin_fmaf((float)field3(w, e), qv[e], acc);
+        return acc;
+    }
+    __device__ static void axpy(const u32x3& w, float ev, float* o) {
+#pragma unroll
+        for (int e = 0; e < 32; ++e) o[e] = __builtin_fmaf(ev, (float)field3(w, e), o[e]);
+    }
+};
+
+// -------------------------------------------------------- tiled ("+") kernel --
+template <int KIND, int D, int G>
+__global__ __launch_bounds__(256) void decode_tiled(DecodeArgs a) {
+    using T = Tile<KIND, D>;
+    using C = Codec<KIND>;
+    using LoadT = typename LaneLoad<KIND>::type;
+    constexpr int ROWB = T::ROWB, LB = T::LB, LP = T::LP, PPW = T::PPW, EPL = T::EPL;
+    static_assert(EPL == C::EPL, "codec width");
+    constexpr bool QUANT = KIND != KF16;
+    constexpr int U   = Unroll<KIND, D>::value;
+    constexpr int NG  = D / G;                   // scale groups per row
+    constexpr int TW  = PPW * U;                 // rows per wave per iteration
+    constexpr int TB  = TW * WAVES;              // rows per work-group per iteration
+    constexpr int SCN = QUANT ? TW * NG : 1;     // (k, v) scale pairs per wave tile
+    constexpr int SCL = NG >= 2 ? SCN / 2 : SCN; // lanes that load scales (dwords or halves)
+    static_assert(!QUANT || G % EPL == 0, "a lane's elements share one scale group");
+    static_assert(SCL <= 64, "one scale load per lane per tensor");
+
+    __shared__ uint32_t s_scale[WAVES][SCN];
+    __shared__ float    s_red[WAVES * 4][D + 1];
+    __shared__ float    s_l[WAVES * 4];
+    __shared__ float    s_m[WAVES];
+
+    const int wg   = blockIdx.x;
+    const int h    = wg / a.S;
+    const int s    = wg - h * a.S;
+    const int wave = uniform((int)(threadIdx.x >> 6));
+    const int lane = (int)(threadIdx.x & 63);
+    const int sl   = lane % LP;                  // lane within its row
+    const int pw   = lane / LP;                  // row slot within a wave load
+    const int g    = (sl * EPL) / G;             // scale group of this lane
+
+    const int j0 = s * a.chunk;
+    const int n  = min(a.L - j0, a.chunk);       // rows of this split (<= 0: empty)
+
+    float m = M_INIT, l = 0.f, E = 0.f;
+    float o[EPL];
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) o[e] = 0.f;
+
+    if (n > 0) {
+        const size_t row0 = (size_t)h * a.L + j0;
+        const __amdgpu_buffer_rsrc_t rk = make_rsrc(a.k + row0 * ROWB, (uint32_t)n * ROWB);
+        const __amdgpu_buffer_rsrc_t rv = make_rsrc(a.v + row0 * ROWB, (uint32_t)n * ROWB);
+        __amdgpu_buffer_rsrc_t rsk = rk, rsv = rv;
+        if constexpr (QUANT) {
+            rsk = make_rsrc(a.sk + row0 * NG, (uint32_t)n * NG * 2);
+            rsv = make_rsrc(a.sv + row0 * NG, (uint32_t)n * NG * 2);
+        }
+
+        // q slice of this lane, pre-scaled into log2 units.
+        float qv[EPL];
+        {
+            const u32x4* qp = reinterpret_cast<const u32x4*>(a.q + (size_t)h * D + sl * EPL);
+#pragma unroll
+            for (int c = 0; c < EPL / 8; ++c) {
+                const u32x4 w = qp[c];
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    qv[8 * c + 2 * i]     = h2f_lo(w[i]) * a.qscale;
+                    qv[8 * c + 2 * i + 1] = h2f_hi(w[i]) * a.qscale;
+                }
+            }
+        }
+        float qbias = 0.f;
+        if constexpr (QUANT) {
+#pragma unroll
+            for (int e = 0; e < EPL; ++e) qbias += qv[e];
+            qbias *= CodeBias<KIND>::value;
+        }
+
+        const uint32_t lane_off = (uint32_t)(pw * ROWB + sl * LB);
+        const int niter = (n + TB - 1) / TB;
+
+        // Two register stages (A, B) alternate: while one tile is computed the
+        // next one is already in flight, and no register copy ever waits on it.
+        LoadT ka[U], va_[U], kb[U], vb[U];
+        uint32_t ska = 0, sva = 0, skb = 0, svb = 0;
+
+        // Issue order is pinned (scales, then K, then V) so the prologue and the
+        // loop leave the same pending-load sequence and the waits stay partial.
+        auto load_tile = [&](int it, LoadT* kk, LoadT* vv, uint32_t& sk, uint32_t& sv) {
+            const uint32_t tpos = sgpr((uint32_t)(it * TB + wave * TW));   // wave-uniform
+            __builtin_amdgcn_sched_barrier(0);
+            if constexpr (QUANT) {            // lanes >= SCL repeat the last entry (unused)
+                const uint32_t sidx = (uint32_t)min(lane, SCL - 1);
+                if constexpr (NG >= 2) {
+                    sk = ld32(rsk, sidx * 4, tpos * NG * 2);
+                    sv = ld32(rsv, sidx * 4, tpos * NG * 2);
+                } else {
+                    sk = ld16(rsk, sidx * 2, tpos * 2);
+                    sv = ld16(rsv, sidx * 2, tpos * 2);
+                }
+            }
+#pragma unroll
+            for (int u = 0; u < U; ++u)
+                kk[u] = lane_load<KIND>(rk, lane_off + (uint32_t)(u * PPW * ROWB), tpos * ROWB);
+#pragma unroll
+            for (int u = 0; u < U; ++u)
+                vv[u] = lane_load<KIND>(rv, lane_off + (uint32_t)(u * PPW * ROWB), tpos * ROWB);
+            __builtin_amdgcn_sched_barrier(0);
+        };
+
+        auto stage_scales = [&](uint32_t sk, uint32_t sv) {   // (k | v << 16) pairs in LDS
+            if constexpr (QUANT) {
+                if (lane < SCL) {
+                    if constexpr (NG >= 2) {
+                        s_scale[wave][2 * lane]     = __builtin_amdgcn_perm(sv, sk, 0x05040100u);
+                        s_scale[wave][2 * lane + 1] = __builtin_amdgcn_perm(sv, sk, 0x07060302u);
+                    } else {
+                        s_scale[wave][lane] = (sk & 0xFFFFu) | (sv << 16);
+                    }
+                }
+            }
+        };
+
+        auto compute_tile = [&](int it, const LoadT* kk, const LoadT* vv) {
+            const int rem = uniform(n - it * TB - wave * TW);   // valid rows of this wave tile
+            float sc[U];
+            uint32_t pair[U];
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                const int slot = u * PPW + pw;
+                float d = C::dot(kk[u], qv);
+                pair[u] = 0;
+                if constexpr (QUANT) {
+                    pair[u] = s_scale[wave][slot * NG + g];
+                    d = (d - qbias) * h2f_lo(pair[u]);
+                }
+                d = group_sum<LP>(d);
+                sc[u] = slot < rem ? d : -__builtin_inff();
+            }
+            float tmax = sc[0];
+#pragma unroll
+            for (int u = 1; u < U; ++u) tmax = fmaxf(tmax, sc[u]);
+            if (__builtin_amdgcn_ballot_w64(tmax > m + RESCALE_SLACK)) {
+                const float mn = uniformf(wave_max(fmaxf(m, tmax)));
+                const float c  = fast_exp2(m - mn);
+                l *= c;
+                E *= c;
+#pragma unroll
+                for (int e = 0; e < EPL; ++e) o[e] *= c;
+                m = mn;
+            }
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                const float p = fast_exp2(sc[u] - m);
+                l += p;
+                float ev = p;
+                if constexpr (QUANT) {
+                    ev = p * h2f_hi(pair[u]);
+                    E += ev;
+                }
+                C::axpy(vv[u], ev, o);
+            }
+        };
+
+        // Tiles are processed in pairs. Loads past the end of the split return
+        // zeros without memory traffic and their scores are masked, so the
+        // prefetch after the last tile and the empty tile that completes an
+        // odd count add no traffic and leave (m, l, o) unchanged.
+        const int npair = (niter + 1) / 2;
+        load_tile(0, ka, va_, ska, sva);
+        for (int ip = 0; ip < npair; ++ip) {
+            const int it = 2 * ip;
+            stage_scales(ska, sva);
+            load_tile(it + 1, kb, vb, skb, svb);
+            compute_tile(it, ka, va_);
+            stage_scales(skb, svb);
+            load_tile(it + 2, ka, va_, ska, sva);
+            compute_tile(it + 1, kb, vb);
+        }
+        if constexpr (QUANT) {
+            const float bias = CodeBias<KIND>::value * E;
+#pragma unroll
+            for (int e = 0; e < EPL; ++e) o[e] -= bias;
+        }
+    }
+
+    // ---- work-group merge: slots of a DPP row first, then rows/waves via LDS.
+#pragma unroll
+    for (int off = LP; off < 16; off *= 2) {
+        if (off == 1) { l += dpp<dpp_row_ror(1)>(l); for (int e = 0; e < EPL; ++e) o[e] += dpp<dpp_row_ror(1)>(o[e]); }
+        if (off == 2) { l += dpp<dpp_row_ror(2)>(l); for (int e = 0; e < EPL; ++e) o[e] += dpp<dpp_row_ror(2)>(o[e]); }
+        if (off == 4) { l += dpp<dpp_row_ror(4)>(l); for (int e = 0; e < EPL; ++e) o[e] += dpp<dpp_row_ror(4)>(o[e]); }
+        if (off == 8) { l += dpp<dpp_row_ror(8)>(l); for (int e = 0; e < EPL; ++e) o[e] += dpp<dpp_row_ror(8)>(o[e]); }
+    }
+    const int row = lane >> 4;
+    if ((lane & 15) < LP) {                       // one slot per 16-lane row holds the row sum
+#pragma unroll
+        for (int e = 0; e < EPL; ++e) s_red[wave * 4 + row][sl * EPL + e] = o[e];
+        if (sl == 0) s_l[wave * 4 + row] = l;
+    }
+    if (lane == 0) s_m[wave] = m;
+    __syncthreads();
+    const int t = (int)threadIdx.x;
+    if (t < D) {
+        float M = s_m[0];
+#pragma unroll
+        for (int w = 1; w < WAVES; ++w) M = fmaxf(M, s_m[w]);
+        float f[WAVES];
+#pragma unroll
+        for (int w = 0; w < WAVES; ++w) f[w] = fast_exp2(s_m[w] - M);
+        float acc = 0.f;
+#pragma unroll
+        for (int r = 0; r < WAVES * 4; ++r) acc = __builtin_fmaf(f[r / 4], s_red[r][t], acc);
+        float* slot = a.ws + (size_t)wg * (D + 2);
+        slot[2 + t] = acc;
+        if (t == 0) {
+            float ls = 0.f;
+#pragma unroll
+            for (int r = 0; r < WAVES * 4; ++r) ls = __builtin_fmaf(f[r / 4], s_l[r], ls);
+            slot[0] = M;
+            slot[1] = ls;
+        }
+    }
+}
+
+// ------------------------------------------------------- naive (w1) kernel --
+// One wave64 per position: lane owns dims [lane*P, lane*P+P), P = D/64.
+template <int KIND, int D, int G>
+__global__ __launch_bounds__(256) void decode_w1(DecodeArgs a) {
+    constexpr int P = D / 64;
+    constexpr bool QUANT = KIND != KF16;
+    constexpr int NG = D / G;
+    constexpr int ROWB = RowBytes<KIND, D>::value;
+
+    __shared__ float s_o[WAVES][D];
+    __shared__ float s_l[WAVES];
+    __shared__ float s_m[WAVES];
+
+    const int wg   = blockIdx.x;
+    const int h    = wg / a.S;
+    const int s    = wg - h * a.S;
+    const int wave = (int)(threadIdx.x >> 6);
+    const int lane = (int)(threadIdx.x & 63);
+    const int g    = (lane * P) / G;
+    const int j0   = s * a.chunk;
+    const int j1   = min(a.L, j0 + a.chunk);
+
+    float qv[P];
+#pragma unroll
+    for (int p = 0; p < P; ++p) qv[p] = h2f(a.q[(size_t)h * D + lane * P + p]) * a.qscale;
+
+    float m = M_INIT, l = 0.f, o[P];
+#pragma unroll
+    for (int p = 0; p < P; ++p) o[p] = 0.f;
+
+    for (int j = j0 + wave; j < j1; j += WAVES) {
+        const size_t row = (size_t)h * a.L + j;
+        const uint8_t* kr = a.k + row * ROWB;
+        const uint8_t* vr = a.v + row * ROWB;
+        float kf[P], vf[P];
+        if constexpr (KIND == KF16) {
+            const uint16_t* kh = reinterpret_cast<const uint16_t*>(kr) + lane * P;
+            const uint16_t* vh = reinterpret_cast<const uint16_t*>(vr) + lane * P;
+#pragma unroll
+            for (int p = 0; p < P; ++p) { kf[p] = h2f(kh[p]); vf[p] = h2f(vh[p]); }
+        } else if constexpr (KIND == KQ8) {
+            const int8_t* kb = reinterpret_cast<const int8_t*>(kr) + lane * P;
+            const int8_t* vb = reinterpret_cast<const int8_t*>(vr) + lane * P;
+#pragma unroll
+            for (int p = 0; p < P; ++p) { kf[p] = (float)kb[p]; vf[p] = (float)vb[p]; }
+        } else {                                   // q4: element e in byte e/2, low nibble first
+#pragma unroll
+            for (int p = 0; p < P; ++p) {
+                const int e = lane * P + p;
+                const uint32_t kb = kr[e >> 1], vb = vr[e >> 1];
+                const int sh = (e & 1) * 4;
+                kf[p] = (float)((int)((kb >> sh) & 0xFu) - 8);
+                vf[p] = (float)((int)((vb >> sh) & 0xFu) - 8);
+            }
+        }
+        float acc = 0.f;
+#pragma unroll
+        for (int p = 0; p < P; ++p) acc = __builtin_fmaf(qv[p], kf[p], acc);
+        float vs = 1.f;
+        if constexpr (QUANT) {
+            acc *= h2f(a.sk[row * NG + g]);
+            vs = h2f(a.sv[row * NG + g]);
+        }
+        acc = wave_sum(acc);
+        const float mn = fmaxf(m, acc);
+        const float c  = fast_exp2(m - mn);
+        const float e  = fast_exp2(acc - mn);
+        l = l * c + e;
+        m = mn;
+        const float ev = e * vs;
+#pragma unroll
+        for (int p = 0; p < P; ++p) o[p] = __builtin_fmaf(o[p], c, ev * vf[p]);
+    }
+
+#pragma unroll
+    for (int p = 0; p < P; ++p) s_o[wave][lane * P + p] = o[p];
+    if (lane == 0) { s_m[wave] = m; s_l[wave] = l; }
+    __syncthreads();
+    const int t = (int)threadIdx.x;
+    if (t < D) {
+        float M = s_m[0];
+#pragma unroll
+        for (int w = 1; w < WAVES; ++w) M = fmaxf(M, s_m[w]);
+        float acc = 0.f, ls = 0.f;
+#pragma unroll
+        for (int w = 0; w < WAVES; ++w) {
+            const float f = fast_exp2(s_m[w] - M);
+            acc = __builtin_fmaf(f, s_o[w][t], acc);
+            ls  = __builtin_fmaf(f, s_l[w], ls);
+        }
+        float* slot = a.ws + (size_t)wg * (D + 2);
+        slot[2 + t] = acc;
+        if (t == 0) { slot[0] = M; slot[1] = ls; }
+    }
+}
+
+// ---------------------------------------------------------------- dispatch --
+template <int KIND, int D>
+static int tiled_positions() {
+    return Tile<KIND, D>::PPW * Unroll<KIND, D>::value * WAVES;
+}
+
+int tile_positions(int kind, bool tiled, int D) {
+    if (!tiled) return WAVES;
+    switch (kind) {
+        case KF16: return D == 128 ? tiled_positions<KF16, 128>() : tiled_positions<KF16, 64>();
+        case KQ8:  return D == 128 ? tiled_positions<KQ8, 128>()  : tiled_positions<KQ8, 64>();
+        case KQ4:  return D == 128 ? tiled_positions<KQ4, 128>()  : tiled_positions<KQ4, 64>();
+        default:   return D == 128 ? tiled_positions<KQ3, 128>()  : tiled_positions<KQ3, 64>();
+    }
+}
+
+template <int KIND, int D, int G>
+static hipError_t launch_one(bool tiled, int H, const DecodeArgs& a, hipStream_t st) {
+    const dim3 grid((unsigned)(H * a.S)), block(256);
+    if (tiled) {
+        hipLaunchKernelGGL((decode_tiled<KIND, D, G>), grid, block, 0, st, a);
+    } else {
+        if constexpr (KIND == KQ3) return hipErrorInvalidValue;
+        else hipLaunchKernelGGL((decode_w1<KIND, D, G>), grid, block, 0, st, a);
+    }
+    return hipGetLastError();
+}
+
+template <int KIND, int D>
+static hipError_t launch_g(bool tiled, int H, int G, const DecodeArgs& a, hipStream_t st) {
+    if constexpr (KIND == KF16) return launch_one<KIND, D, 64>(tiled, H, a, st);
+    else return G == 32 ? launch_one<KIND, D, 32>(tiled, H, a, st)
+                        : launch_one<KIND, D, 64>(tiled, H, a, st);
+}
+
+template <int KIND>
+static hipError_t launch_d(bool tiled, int H, int D, int G, const DecodeArgs& a, hipStream_t st) {
+    return D == 128 ? launch_g<KIND, 128>(tiled, H, G, a, st) : launch_g<KIND, 64>(tiled, H, G, a, st);
+}
+
+hipError_t launch_decode(int kind, bool tiled, int H, int D, int G, const DecodeArgs& a,
+                         hipStream_t stream) {
+    switch (kind) {
+        case KF16: return launch_d<KF16>(tiled, H, D, G, a, stream);
+        case KQ8:  return launch_d<KQ8>(tiled, H, D, G, a, stream);
+        case KQ4:  return launch_d<KQ4>(tiled, H, D, G, a, stream);
+        case KQ3:  return launch_d<KQ3>(tiled, H, D, G, a, stream);
+        default:   return hipErrorInvalidValue;
+    }
+}
+
+} // namespace va

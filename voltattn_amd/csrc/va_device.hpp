@@ -1,0 +1,138 @@
+// va_device.hpp — gfx950 device helpers shared by the decode, merge, probe and
+// quantize kernels. CDNA4 only: wave64, raw buffer loads, DPP row ops.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace va {
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x3 __attribute__((ext_vector_type(3)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef float    f32x4 __attribute__((ext_vector_type(4)));
+
+// Payload kinds. f16 / q8 / q4 / q3 are the reference's storage formats
+// (src/voltattn.cu:676-692); "+" vs naive is a kernel choice, not a kind.
+enum Kind : int { KF16 = 0, KQ8 = 1, KQ4 = 2, KQ3 = 3 };
+
+template <int KIND> struct KindBits;
+template <> struct KindBits<KF16> { static constexpr int num = 16; };
+template <> struct KindBits<KQ8>  { static constexpr int num = 8; };
+template <> struct KindBits<KQ4>  { static constexpr int num = 4; };
+template <> struct KindBits<KQ3>  { static constexpr int num = 3; };
+
+// Bytes of one D-element row of a kind.
+template <int KIND, int D> struct RowBytes {
+    static constexpr int value = D * KindBits<KIND>::num / 8;
+};
+
+// Offset added to stored codes to make them unsigned (q8 is stored signed and
+// flipped by xor 0x80; q4 nibbles hold v+8; q3 fields hold v+4).
+template <int KIND> struct CodeBias;
+template <> struct CodeBias<KF16> { static constexpr float value = 0.f; };
+template <> struct CodeBias<KQ8>  { static constexpr float value = 128.f; };
+template <> struct CodeBias<KQ4>  { static constexpr float value = 8.f; };
+template <> struct CodeBias<KQ3>  { static constexpr float value = 4.f; };
+
+// ------------------------------------------------------------ buffer loads --
+// Raw buffer resource: base, no stride, `bytes` records. A load whose offset
+// lies at or beyond `bytes` returns zeros without touching memory, which is
+// how partial tiles at the end of a split are handled.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes,
+                                             0x00020000);
+}
+
+// `soff` must be wave-uniform; it is pinned to an SGPR with readfirstlane so
+// the compiler never wraps the load in a per-lane (waterfall) loop.
+__device__ __forceinline__ uint32_t sgpr(uint32_t x) {
+    return (uint32_t)__builtin_amdgcn_readfirstlane((int)x);
+}
+__device__ __forceinline__ u32x4 ld128(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+    return __builtin_amdgcn_raw_buffer_load_b128(r, voff, sgpr(soff), 0);
+}
+__device__ __forceinline__ u32x3 ld96(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+    return __builtin_amdgcn_raw_buffer_load_b96(r, voff, sgpr(soff), 0);
+}
+__device__ __forceinline__ uint32_t ld32(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+    return __builtin_amdgcn_raw_buffer_load_b32(r, voff, sgpr(soff), 0);
+}
+__device__ __forceinline__ uint32_t ld16(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+    return (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(r, voff, sgpr(soff), 0);
+}
+
+// ------------------------------------------------------------------ scalars --
+__device__ __forceinline__ int uniform(int x) { return __builtin_amdgcn_readfirstlane(x); }
+__device__ __forceinline__ float uniformf(float x) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, x)));
+}
+
+// 2^x on the VALU transcendental unit (v_exp_f32). exp2(-inf) = 0.
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+__device__ __forceinline__ float h2f(uint32_t bits16) {
+    return (float)__builtin_bit_cast(_Float16, (uint16_t)bits16);
+}
+__device__ __forceinline__ float h2f_lo(uint32_t w) { return h2f(w & 0xFFFFu); }
+__device__ __forceinline__ float h2f_hi(uint32_t w) { return h2f(w >> 16); }
+__device__ __forceinline__ uint16_t f2h_rne(float x) {
+    return __builtin_bit_cast(uint16_t, (_Float16)x);   // v_cvt_f16_f32, RNE mode
+}
+
+// --------------------------------------------------------------- DPP / swizzle --
+// dpp_ctrl encodings (GCN3+ DPP): quad_perm, row rotate right, row mirrors.
+constexpr int DPP_QP_XOR1 = 0xB1;       // quad_perm [1,0,3,2]
+constexpr int DPP_QP_XOR2 = 0x4E;       // quad_perm [2,3,0,1]
+constexpr int DPP_ROW_HALF_MIRROR = 0x141;
+constexpr int DPP_ROW_MIRROR = 0x140;
+constexpr int dpp_row_ror(int n) { return 0x120 + n; }   // n in 1..15
+
+template <int CTRL>
+__device__ __forceinline__ float dpp(float x) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x),
+                                                                 CTRL, 0xF, 0xF, false));
+}
+
+// Sum over aligned groups of N consecutive lanes (N in 1,2,4,8,16); every lane
+// of the group receives the group total. Butterfly inside a DPP row: xor 1,
+// xor 2, then half-row and full-row mirrors (each mirror pairs sub-blocks whose
+// members already hold equal partial sums).
+template <int N>
+__device__ __forceinline__ float group_sum(float x) {
+    static_assert(N == 1 || N == 2 || N == 4 || N == 8 || N == 16, "group size");
+    if constexpr (N >= 2)  x += dpp<DPP_QP_XOR1>(x);
+    if constexpr (N >= 4)  x += dpp<DPP_QP_XOR2>(x);
+    if constexpr (N >= 8)  x += dpp<DPP_ROW_HALF_MIRROR>(x);
+    if constexpr (N >= 16) x += dpp<DPP_ROW_MIRROR>(x);
+    return x;
+}
+
+// ds_swizzle bit-mask mode: lane i reads lane ((i & and) | or) ^ xor within 32.
+template <int XOR_MASK>
+__device__ __forceinline__ float swz_xor(float x) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, x),
+                                                                 0x1F | (XOR_MASK << 10)));
+}
+__device__ __forceinline__ float lane_xor32(float x) {
+    const int src = ((int)__lane_id() ^ 32) << 2;
+    return __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute(src, __builtin_bit_cast(int, x)));
+}
+
+// Full-wave max and sum (all 64 lanes receive the result).
+__device__ __forceinline__ float wave_max(float x) {
+    x = fmaxf(x, dpp<DPP_QP_XOR1>(x));
+    x = fmaxf(x, dpp<DPP_QP_XOR2>(x));
+    x = fmaxf(x, dpp<DPP_ROW_HALF_MIRROR>(x));
+    x = fmaxf(x, dpp<DPP_ROW_MIRROR>(x));
+    x = fmaxf(x, swz_xor<16>(x));
+    x = fmaxf(x, lane_xor32(x));
+    return x;
+}
+__device__ __forceinline__ float wave_sum(float x) {
+    x = group_sum<16>(x);
+    x += swz_xor<16>(x);
+    x += lane_xor32(x);
+    return x;
+}
+
+} // namespace va

@@ -1,0 +1,165 @@
+// va_quant.hip — device-side producers of the decode path's inputs:
+//   * quantize_groups: the symmetric per-group quantizer + packer, bit-exact
+//     with the reference's host quantize() (src/voltattn.cu:705-745) for
+//     G in {32, 64}: amax in fp32, s = amax/lim (IEEE division), the fp16
+//     scale rounded to nearest even, codes clamp(rint(x / float(scale))), with
+//     a non-finite quotient giving code 0 as x86-64 lrint + int truncation does;
+//   * f32_to_f16: round-to-nearest-even conversion of fp32 arrays (the
+//     reference's __float2half over the f16-format K/V, src/voltattn.cu:866-868);
+//   * fill_normal: seeded N(0,1) bench data, Philox4x32-10 (Salmon et al.,
+//     SC'11) counters through the Box-Muller transform.
+#include "va_device.hpp"
+#include "va_kernels.hpp"
+
+namespace va {
+
+template <int BITS> struct QLim;
+template <> struct QLim<8> { static constexpr int value = 127; };
+template <> struct QLim<4> { static constexpr int value = 7; };
+template <> struct QLim<3> { static constexpr int value = 3; };
+
+// One thread per quantization group of G consecutive elements. Groups are
+// contiguous: group r*(D/G) + g starts at element (r*(D/G) + g) * G.
+template <int BITS, int G>
+__global__ __launch_bounds__(256) void quantize_groups(const float* __restrict__ x, size_t ngroups,
+                                                       uint8_t* __restrict__ packed,
+                                                       uint16_t* __restrict__ scales) {
+    constexpr int lim = QLim<BITS>::value;
+    const size_t stride = (size_t)gridDim.x * blockDim.x;
+    for (size_t gi = (size_t)blockIdx.x * blockDim.x + threadIdx.x; gi < ngroups; gi += stride) {
+        const f32x4* xp = reinterpret_cast<const f32x4*>(x + gi * G);
+        float xv[G];
+#pragma unroll
+        for (int c = 0; c < G / 4; ++c) {
+            const f32x4 w = xp[c];
+            xv[4 * c] = w.x; xv[4 * c + 1] = w.y; xv[4 * c + 2] = w.z; xv[4 * c + 3] = w.w;
+        }
+        float amax = 0.f;
+#pragma unroll
+        for (int i = 0; i < G; ++i) amax = fmaxf(amax, __builtin_fabsf(xv[i]));
+        const float s = amax > 0.f ? amax / (float)lim : 1.f;
+        const uint16_t sb = f2h_rne(s);
+        const float sh = h2f(sb);
+        int code[G];
+#pragma unroll
+        for (int i = 0; i < G; ++i) {
+            const float t = xv[i] / sh;
+            int v = __builtin_isfinite(t) ? (int)__builtin_rintf(t) : 0;
+            v = v < -lim ? -lim : (v > lim ? lim : v);
+            code[i] = v;
+        }
+        scales[gi] = sb;
+        if constexpr (BITS == 8) {
+            uint32_t* dst = reinterpret_cast<uint32_t*>(packed + gi * G);
+#pragma unroll
+            for (int k = 0; k < G / 4; ++k) {
+                uint32_t w = 0;
+#pragma unroll
+                for (int b = 0; b < 4; ++b) w |= (uint32_t)(uint8_t)(int8_t)code[4 * k + b] << (8 * b);
+                dst[k] = w;
+            }
+        } else if constexpr (BITS == 4) {         // element i: byte i/2, low nibble when i even
+            uint32_t* dst = reinterpret_cast<uint32_t*>(packed + gi * (G / 2));
+#pragma unroll
+            for (int k = 0; k < G / 8; ++k) {
+                uint32_t w = 0;
+#pragma unroll
+                for (int i = 0; i < 8; ++i) w |= (uint32_t)(code[8 * k + i] + 8) << (4 * i);
+                dst[k] = w;
+            }
+        } else {                                   // element i: bits [3i, 3i+3), little endian
+            constexpr int NW = 3 * G / 32;
+            uint32_t w[NW];
+#pragma unroll
+            for (int k = 0; k < NW; ++k) w[k] = 0;
+#pragma unroll
+            for (int i = 0; i < G; ++i) {
+                const uint32_t c = (uint32_t)(code[i] + 4);
+                const int b = 3 * i;
+                w[b / 32] |= c << (b % 32);
+                if (b % 32 > 29) w[b / 32 + 1] |= c >> (32 - b % 32);
+            }
+            uint32_t* dst = reinterpret_cast<uint32_t*>(packed + gi * (3 * G / 8));
+#pragma unroll
+            for (int k = 0; k < NW; ++k) dst[k] = w[k];
+        }
+    }
+}
+
+__global__ __launch_bounds__(256) void f32_to_f16_kernel(const float* __restrict__ x, size_t n,
+                                                         uint16_t* __restrict__ out) {
+    const size_t stride = (size_t)gridDim.x * blockDim.x;
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride)
+        out[i] = f2h_rne(x[i]);
+}
+
+// Philox4x32-10 block: counter (c0..c3), key (k0, k1).
+__device__ __forceinline__ u32x4 philox4x32_10(u32x4 c, uint32_t k0, uint32_t k1) {
+    constexpr uint32_t M0 = 0xD2511F53u, M1 = 0xCD9E8D57u;
+    constexpr uint32_t W0 = 0x9E3779B9u, W1 = 0xBB67AE85u;
+#pragma unroll
+    for (int r = 0; r < 10; ++r) {
+        const uint32_t hi0 = __umulhi(M0, c.x), lo0 = M0 * c.x;
+        const uint32_t hi1 = __umulhi(M1, c.z), lo1 = M1 * c.z;
+        c = u32x4{hi1 ^ c.y ^ k0, lo1, hi0 ^ c.w ^ k1, lo0};
+        k0 += W0;
+        k1 += W1;
+    }
+    return c;
+}
+
+__global__ __launch_bounds__(256) void fill_normal_kernel(float* __restrict__ x, size_t n,
+                                                          uint32_t k0, uint32_t k1) {
+    const size_t stride = (size_t)gridDim.x * blockDim.x;
+    const size_t nblk = (n + 3) / 4;
+    for (size_t b = (size_t)blockIdx.x * blockDim.x + threadIdx.x; b < nblk; b += stride) {
+        const u32x4 r = philox4x32_10(u32x4{(uint32_t)b, (uint32_t)(b >> 32), 0u, 0u}, k0, k1);
+        float z[4];
+#pragma unroll
+        for (int p = 0; p < 2; ++p) {
+            const uint32_t a = p ? r.z : r.x, c = p ? r.w : r.y;
+            const float u1 = (float)((a >> 8) + 1u) * 5.9604644775390625e-8f;  // (0, 1]
+            const float u2 = (float)(c >> 8) * 5.9604644775390625e-8f;         // [0, 1)
+            const float rad = sqrtf(-2.f * logf(u1));
+            float sn, cs;
+            sincosf(6.28318530717958648f * u2, &sn, &cs);
+            z[2 * p] = rad * cs;
+            z[2 * p + 1] = rad * sn;
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            if (4 * b + i < n) x[4 * b + i] = z[i];
+    }
+}
+
+static unsigned grid_for(size_t work) {
+    const size_t blocks = (work + 255) / 256;
+    return (unsigned)(blocks < 16384 ? (blocks ? blocks : 1) : 16384);
+}
+
+hipError_t launch_quantize(int bits, int G, const float* x, size_t rows, int D, uint8_t* packed,
+                           uint16_t* scales, hipStream_t stream) {
+    const size_t ngroups = rows * (size_t)(D / G);
+    const dim3 grid(grid_for(ngroups)), block(256);
+#define VA_QLAUNCH(B, GG) hipLaunchKernelGGL((quantize_groups<B, GG>), grid, block, 0, stream, x, ngroups, packed, scales)
+    if (G == 32) {
+        if (bits == 8) VA_QLAUNCH(8, 32); else if (bits == 4) VA_QLAUNCH(4, 32); else VA_QLAUNCH(3, 32);
+    } else {
+        if (bits == 8) VA_QLAUNCH(8, 64); else if (bits == 4) VA_QLAUNCH(4, 64); else VA_QLAUNCH(3, 64);
+    }
+#undef VA_QLAUNCH
+    return hipGetLastError();
+}
+
+hipError_t launch_f32_to_f16(const float* x, size_t n, uint16_t* out, hipStream_t stream) {
+    hipLaunchKernelGGL(f32_to_f16_kernel, dim3(grid_for(n)), dim3(256), 0, stream, x, n, out);
+    return hipGetLastError();
+}
+
+hipError_t launch_fill_normal(float* x, size_t n, uint64_t seed, hipStream_t stream) {
+    hipLaunchKernelGGL(fill_normal_kernel, dim3(grid_for((n + 3) / 4)), dim3(256), 0, stream, x, n,
+                       (uint32_t)seed, (uint32_t)(seed >> 32));
+    return hipGetLastError();
+}
+
+} // namespace va
