@@ -169,6 +169,16 @@ int va_event_record(void* ev, void* stream);
 int va_event_sync(void* ev);
 int va_event_elapsed_ms(void* start, void* stop, float* ms);
 
+/* HIP graph capture of a launch sequence on a (non-default) stream: the
+ * reference launches every step from the host; a serving loop would replay
+ * captured decode steps instead. va_graph_end instantiates the captured work;
+ * va_graph_launch replays it on `stream`. No memset nodes are captured by any
+ * entry point of this library. */
+int va_graph_begin(void* stream);
+int va_graph_end(void* stream, void** graph_exec);
+int va_graph_launch(void* graph_exec, void* stream);
+int va_graph_destroy(void* graph_exec);
+
 /* Message of the calling thread's last failure ("" if none). */
 const char* va_last_error(void);
 

@@ -2,7 +2,7 @@
 
 Python mirror of kamilch1k/voltattn's host interface over the C ABI of
 ``include/voltattn.h`` (``libvoltattn_hip.so``, built in-tree by
-``python -m voltattn_amd.build``):
+``python voltattn_amd/build.py``):
 
 * :class:`Fmt` — the reference's ``enum class Fmt`` (src/voltattn.cu:676);
 * :class:`DeviceBufs` — ``struct DeviceBufs`` (src/voltattn.cu:796-801);
@@ -17,6 +17,7 @@ from __future__ import annotations
 
 import ctypes as C
 import enum
+import os
 from dataclasses import dataclass
 from pathlib import Path
 
@@ -26,13 +27,14 @@ __all__ = [
     "Fmt", "DeviceBufs", "VAError", "launch", "decode_splits", "merge", "ws_bytes",
     "payload_bytes", "scale_bytes", "split_chunk", "pick_splits", "quantize", "f32_to_f16",
     "fill_normal", "probe_read", "device_info", "device_count", "DeviceBuffer", "Event",
-    "Stream", "sync", "lib", "LIB_PATH", "fmt_bits", "is_f16",
+    "Stream", "Graph", "sync", "lib", "LIB_PATH", "fmt_bits", "is_f16", "check",
 ]
 
-LIB_PATH = Path(__file__).resolve().parent / "libvoltattn_hip.so"
+# VOLTATTN_LIB may name another build of the same library (tuning variants).
+LIB_PATH = Path(os.environ.get("VOLTATTN_LIB") or Path(__file__).resolve().parent / "libvoltattn_hip.so")
 if not LIB_PATH.exists():
     raise ImportError(
-        f"{LIB_PATH} is not built; run `python -m voltattn_amd.build` (needs hipcc for gfx950)")
+        f"{LIB_PATH} is not built; run `python voltattn_amd/build.py` (needs hipcc for gfx950)")
 lib = C.CDLL(str(LIB_PATH))
 
 _P, _I, _SZ, _U64 = C.c_void_p, C.c_int, C.c_size_t, C.c_uint64
@@ -86,6 +88,10 @@ _sig("va_event_destroy", _I, _P)
 _sig("va_event_record", _I, _P, _P)
 _sig("va_event_sync", _I, _P)
 _sig("va_event_elapsed_ms", _I, _P, _P, C.POINTER(C.c_float))
+_sig("va_graph_begin", _I, _P)
+_sig("va_graph_end", _I, _P, C.POINTER(_P))
+_sig("va_graph_launch", _I, _P, _P)
+_sig("va_graph_destroy", _I, _P)
 _sig("va_last_error", C.c_char_p)
 _sig("va_abi_version", _I)
 
@@ -308,3 +314,40 @@ class Event:
         if self.handle:
             check(lib.va_event_destroy(self.handle))
             self.handle = 0
+
+
+class Graph:
+    """A captured launch sequence: `with Graph.capture(stream) as g: ...` then g.launch(stream)."""
+
+    def __init__(self, handle: int):
+        self.handle = handle
+
+    @classmethod
+    def capture(cls, stream: "Stream"):
+        return _Capture(stream)
+
+    def launch(self, stream=None) -> None:
+        check(lib.va_graph_launch(self.handle, _stream(stream)))
+
+    def destroy(self) -> None:
+        if self.handle:
+            check(lib.va_graph_destroy(self.handle))
+            self.handle = 0
+
+
+class _Capture:
+    def __init__(self, stream: "Stream"):
+        self.stream = stream
+        self.graph: Graph | None = None
+
+    def __enter__(self) -> "_Capture":
+        check(lib.va_graph_begin(_stream(self.stream)))
+        return self
+
+    def __exit__(self, exc_type, exc, tb):
+        h = _P()
+        rc = lib.va_graph_end(_stream(self.stream), C.byref(h))
+        if exc_type is None:
+            check(rc)
+            self.graph = Graph(int(h.value))
+        return False

@@ -1,6 +1,8 @@
 """Build recipe for the in-tree native artefacts.
 
-    python -m voltattn_amd.build            # library + oracle + CLI harness
+    python voltattn_amd/build.py            # library + oracle + CLI harness
+
+(run as a file, not ``-m``: importing the package loads the library being built)
 
 * ``voltattn_amd/libvoltattn_hip.so`` — the product: gfx950 HIP kernels and the
   C ABI of ``include/voltattn.h`` (hipcc, one object per ``csrc/*.hip``).
@@ -54,22 +56,27 @@ def _run(cmd: list[str], cwd: Path | None = None) -> None:
         raise RuntimeError(f"command failed ({res.returncode}): {' '.join(cmd)}\n{res.stdout}\n{res.stderr}")
 
 
-def build_library(jobs: int = 8) -> Path:
-    OBJ.mkdir(parents=True, exist_ok=True)
+def build_library(jobs: int = 8, out: Path = LIB, defines: tuple[str, ...] = ()) -> Path:
+    """Compile csrc/*.hip and link `out`; `defines` (e.g. "VA_LOAD_AUX=2") build a variant."""
+    obj_dir = OBJ if not defines else OBJ / ("v_" + "_".join(d.replace("=", "") for d in defines))
+    obj_dir.mkdir(parents=True, exist_ok=True)
     srcs = sorted(CSRC.glob("*.hip"))
     cc = hipcc()
+    dflags = [f"-D{d}" for d in defines]
 
     def compile_one(src: Path) -> Path:
-        obj = OBJ / (src.stem + ".o")
-        _run([cc, *HIPCC_FLAGS, "-I", str(ROOT / "include"), "-c", str(src), "-o", str(obj)])
+        obj = obj_dir / (src.stem + ".o")
+        _run([cc, *HIPCC_FLAGS, *dflags, "-I", str(ROOT / "include"), "-c", str(src), "-o", str(obj)])
         return obj
 
     with cf.ThreadPoolExecutor(max_workers=max(1, jobs)) as ex:
         objs = list(ex.map(compile_one, srcs))
-    tmp = LIB.with_suffix(".so.tmp")
+    out = Path(out)
+    out.parent.mkdir(parents=True, exist_ok=True)
+    tmp = out.with_suffix(".so.tmp")
     _run([cc, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *map(str, objs)])
-    os.replace(tmp, LIB)
-    return LIB
+    os.replace(tmp, out)
+    return out
 
 
 def build_oracle() -> Path:

@@ -23,10 +23,11 @@
 // stay <= 2^RESCALE_SLACK and most tiles skip the rescale entirely. (o, l, m)
 // always describe the same normalised value, so the result is unchanged.
 //
-// Quantized codes are consumed unsigned (q8 xor 0x80, q4 nibble, q3 field)
-// with v_cvt_f32_ubyte; the constant code offset is removed once: from the
-// score via the lane's sum of q, and from o via the running sum of the
-// weights (E), so the inner loop has no per-element subtraction.
+// q8 and q3 codes are consumed unsigned (q8 xor 0x80, q3 field) with one
+// convert each; their constant offset is removed once: from the score via the
+// lane's sum of q, and from o via the running sum of the weights (E). q4 codes
+// become exact fp16 values two at a time and feed v_dot2_f32_f16 (K) and
+// v_fma_mix_f32 (V); see Codec<KQ4>.
 //
 // Naive kernels (f16, q8, q4): one wave64 per position, D/64 elements per
 // lane, a 6-step cross-lane sum and an exact per-position online-softmax
@@ -35,11 +36,100 @@
 #include "va_device.hpp"
 #include "va_kernels.hpp"
 
+#include <cstdlib>
+
 namespace va {
 
 constexpr int WAVES = 4;                 // waves per work-group
 constexpr float RESCALE_SLACK = 8.0f;    // log2 units: weights stay <= 256
 constexpr float M_INIT = -1e30f;         // finite "no score yet" maximum
+constexpr float M_FLOOR = -3.0e38f;      // below every partial's m
+
+// Arrival counters of the fused merge (zero-initialised with the code object).
+__device__ __align__(256) unsigned g_tickets[TICKET_SLOTS * TICKET_MAXH * TICKET_STRIDE];
+
+// Log-sum-exp merge of one head's S partials by a whole work-group (256
+// threads): thread (d, sg) folds splits sg, sg + 256/D, ... with a running
+// maximum, eight loads in flight per round; the split groups are then combined
+// through LDS. Same algebra as the standalone merge pass (va_merge.hip).
+template <int D>
+__device__ void block_merge(const float* __restrict__ base, int S, uint16_t* __restrict__ outh) {
+    constexpr int NSG = 256 / D;
+    constexpr int PT  = 8;
+    __shared__ float s_acc[NSG][D];
+    __shared__ float s_lg[NSG];
+    __shared__ float s_mw[WAVES];
+    const int t = (int)threadIdx.x, d = t % D, sg = t / D;
+    const size_t stride = (size_t)(D + 2);
+    float mt = M_FLOOR, acc = 0.f, lacc = 0.f;
+    for (int s0 = sg; s0 < S; s0 += NSG * PT) {
+        float mv[PT], lv[PT], ov[PT];
+#pragma unroll
+        for (int i = 0; i < PT; ++i) {
+            const int s = s0 + NSG * i;
+            const bool ok = s < S;
+            const float* slot = base + (size_t)(ok ? s : 0) * stride;
+            mv[i] = ok ? load_dev(slot) : M_FLOOR;
+            lv[i] = ok ? load_dev(slot + 1) : 0.f;
+            ov[i] = ok ? load_dev(slot + 2 + d) : 0.f;
+        }
+        float mr = mt;
+#pragma unroll
+        for (int i = 0; i < PT; ++i) mr = fmaxf(mr, mv[i]);
+        const float c = fast_exp2(mt - mr);
+        acc *= c;
+        lacc *= c;
+#pragma unroll
+        for (int i = 0; i < PT; ++i) {
+            const float w = fast_exp2(mv[i] - mr);
+            acc  = __builtin_fmaf(w, ov[i], acc);
+            lacc = __builtin_fmaf(w, lv[i], lacc);
+        }
+        mt = mr;
+    }
+    const float wm = wave_max(mt);
+    if ((t & 63) == 0) s_mw[t >> 6] = wm;
+    __syncthreads();
+    float M = s_mw[0];
+#pragma unroll
+    for (int w = 1; w < WAVES; ++w) M = fmaxf(M, s_mw[w]);
+    const float f = fast_exp2(mt - M);
+    s_acc[sg][d] = acc * f;
+    if (d == 0) s_lg[sg] = lacc * f;
+    __syncthreads();
+    if (t < D) {
+        float o = 0.f, l = 0.f;
+#pragma unroll
+        for (int g = 0; g < NSG; ++g) {
+            o += s_acc[g][t];
+            l += s_lg[g];
+        }
+        outh[t] = f2h_rne(o / l);
+    }
+}
+
+// Fused second pass: after a work-group has written its partial, the group
+// that completes head h (the S-th arrival on the head's counter) merges all S
+// partials and resets the counter. Partials are stored and loaded with
+// device-scope coherent accesses (store_dev/load_dev), and every thread waits
+// for its stores to complete before the barrier that precedes the ticket
+// increment, so the merging group reads every partial from the coherence
+// point without any L2 writeback or invalidate.
+template <int D>
+__device__ void fused_merge(const DecodeArgs& a, int h) {
+    if (a.ticket_slot < 0) return;
+    __shared__ int s_last;
+    wait_all_mem();
+    __syncthreads();
+    unsigned* ticket = g_tickets + ((size_t)a.ticket_slot * TICKET_MAXH + h) * TICKET_STRIDE;
+    if (threadIdx.x == 0)
+        s_last = __hip_atomic_fetch_add(ticket, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+                 (unsigned)(a.S - 1);
+    __syncthreads();
+    if (!s_last) return;
+    block_merge<D>(a.ws + (size_t)h * a.S * (D + 2), a.S, a.out + (size_t)h * D);
+    if (threadIdx.x == 0) __hip_atomic_store(ticket, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
 
 // --------------------------------------------------------------- layouts ----
 template <int KIND, int D> struct Tile {
@@ -51,8 +141,13 @@ template <int KIND, int D> struct Tile {
     static_assert(ROWB % LB == 0 && 64 % LP == 0 && LP <= 16, "lane split");
 };
 
-// Rows per lane in flight per tile (per tensor).
-template <int KIND, int D> struct Unroll { static constexpr int value = KIND == KF16 ? 4 : 2; };
+// Rows per lane per tile and tensor (U). Each kind is instantiated for two
+// depths; va_unroll() picks one at run time (default: the first).
+template <int KIND> struct UnrollSet;
+template <> struct UnrollSet<KF16> { static constexpr int a = 4, b = 8; };
+template <> struct UnrollSet<KQ8>  { static constexpr int a = 2, b = 4; };
+template <> struct UnrollSet<KQ4>  { static constexpr int a = 2, b = 4; };
+template <> struct UnrollSet<KQ3>  { static constexpr int a = 2, b = 4; };
 
 template <int KIND> struct LaneLoad { using type = u32x4; };
 template <> struct LaneLoad<KQ3> { using type = u32x3; };
@@ -78,21 +173,39 @@ __device__ __forceinline__ uint32_t field3(const u32x3& w, int e) {
     return (w.z >> (b - 64)) & 7u;
 }
 
-// Per-kind lane codec: dot(q, codes) and o += ev * codes over EPL elements.
+// Per-kind lane codec over the EPL elements a lane owns in one row:
+//   QReg       the lane's slice of q in the form the codec consumes;
+//   load_q     q (fp16, 16-byte aligned lane slice) -> QReg; qs = log2(e)/sqrt(D);
+//   dot        sum_e q_e * code_e in log2 units (q pre-scaled), any code offset removed;
+//   axpy       o_e += ev * code_e (code still offset by VBIAS, if nonzero);
+//   VBIAS      offset left in the V codes; the kernel removes VBIAS * sum(ev) once.
+typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ h2 as_h2(uint32_t x) { return __builtin_bit_cast(h2, x); }
+
 template <int KIND> struct Codec;
 
 template <> struct Codec<KF16> {                 // 8 halves per lane
     static constexpr int EPL = 8;
-    __device__ static float dot(const u32x4& w, const float* qv) {
+    static constexpr float VBIAS = 0.f;
+    struct QReg { float q[8]; };
+    __device__ static void load_q(QReg& r, const uint16_t* qh, float qs) {
+        const u32x4 w = *reinterpret_cast<const u32x4*>(qh);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            r.q[2 * i]     = h2f_lo(w[i]) * qs;
+            r.q[2 * i + 1] = h2f_hi(w[i]) * qs;
+        }
+    }
+    __device__ static float dot(const u32x4& w, const QReg& r) {
         float acc = 0.f;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            acc = __builtin_fmaf(h2f_lo(w[i]), qv[2 * i], acc);
-            acc = __builtin_fmaf(h2f_hi(w[i]), qv[2 * i + 1], acc);
+            acc = __builtin_fmaf(h2f_lo(w[i]), r.q[2 * i], acc);
+            acc = __builtin_fmaf(h2f_hi(w[i]), r.q[2 * i + 1], acc);
         }
         return acc;
     }
-    __device__ static void axpy(const u32x4& w, float ev, float* o) {
+    __device__ static void axpy(const u32x4& w, float ev, float* o, const QReg&) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             o[2 * i]     = __builtin_fmaf(ev, h2f_lo(w[i]), o[2 * i]);
@@ -103,17 +216,34 @@ template <> struct Codec<KF16> {                 // 8 halves per lane
 
 template <> struct Codec<KQ8> {                  // 16 int8 per lane, consumed as u8 = v + 128
     static constexpr int EPL = 16;
-    __device__ static float dot(const u32x4& w, const float* qv) {
+    static constexpr float VBIAS = 128.f;
+    struct QReg { float q[16]; float qbias; };
+    __device__ static void load_q(QReg& r, const uint16_t* qh, float qs) {
+        r.qbias = 0.f;
+#pragma unroll
+        for (int c = 0; c < 2; ++c) {
+            const u32x4 w = reinterpret_cast<const u32x4*>(qh)[c];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                r.q[8 * c + 2 * i]     = h2f_lo(w[i]) * qs;
+                r.q[8 * c + 2 * i + 1] = h2f_hi(w[i]) * qs;
+            }
+        }
+#pragma unroll
+        for (int e = 0; e < 16; ++e) r.qbias += r.q[e];
+        r.qbias *= 128.f;
+    }
+    __device__ static float dot(const u32x4& w, const QReg& r) {
         float acc = 0.f;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const uint32_t u = w[i] ^ 0x80808080u;
 #pragma unroll
-            for (int b = 0; b < 4; ++b) acc = __builtin_fmaf(ubyte(u, b), qv[4 * i + b], acc);
+            for (int b = 0; b < 4; ++b) acc = __builtin_fmaf(ubyte(u, b), r.q[4 * i + b], acc);
         }
-        return acc;
+        return acc - r.qbias;
     }
-    __device__ static void axpy(const u32x4& w, float ev, float* o) {
+    __device__ static void axpy(const u32x4& w, float ev, float* o, const QReg&) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const uint32_t u = w[i] ^ 0x80808080u;
@@ -124,52 +254,106 @@ template <> struct Codec<KQ8> {                  // 16 int8 per lane, consumed a
     }
 };
 
-template <> struct Codec<KQ4> {                  // 32 nibbles per lane (v + 8), low nibble first
+// q4: 32 nibbles per lane; element 8i+j of the lane sits in nibble j of dword i.
+// Each dword becomes four exact fp16 pairs: OR-ing a nibble into the mantissa
+// of 1024.0 (0x6400) gives 1024 + n (or 1024 + 16n for a high nibble left in
+// place), and one packed subtract of 1032 (1152) leaves v = n - 8 (16v):
+//   P0 = (e0, e4) = v,  P1 = (e1, e5) = 16v,  P2 = (e2, e6) = v,  P3 = (e3, e7) = 16v
+// (P2/P3 from the dword shifted right by 8). Every value is an exact small
+// integer, so K is consumed by v_dot2_f32_f16 against the unscaled fp16 q
+// (exact products, fp32 accumulation; the 16v pairs in a second accumulator
+// scaled by 1/16 at the end) and V by v_fma_mix_f32 (fp16 operand, fp32 FMA).
+template <> struct Codec<KQ4> {
     static constexpr int EPL = 32;
-    __device__ static float dot(const u32x4& w, const float* qv) {
-        float acc = 0.f;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const uint32_t lo = w[i] & 0x0F0F0F0Fu;          // elements 8i + 2b
-            const uint32_t hi = (w[i] >> 4) & 0x0F0F0F0Fu;   // elements 8i + 2b + 1
-#pragma unroll
-            for (int b = 0; b < 4; ++b) {
-                acc = __builtin_fmaf(ubyte(lo, b), qv[8 * i + 2 * b], acc);
-                acc = __builtin_fmaf(ubyte(hi, b), qv[8 * i + 2 * b + 1], acc);
-            }
-        }
-        return acc;
+    static constexpr float VBIAS = 0.f;
+    // magic: 0x64006400 held in a VGPR, so the mask-and-insert is one
+    // v_and_or_b32 (a gfx9 VOP3 takes one scalar constant; mask and magic
+    // cannot both be literals).
+    struct QReg { h2 q0[4], q1[4], q2[4], q3[4]; float qs; uint32_t magic; };
+    __device__ static void pairs(uint32_t w, uint32_t magic, h2& p0, h2& p1, h2& p2, h2& p3) {
+        const uint32_t w8 = w >> 8;
+        p0 = as_h2((w & 0x000F000Fu) | magic) - h2{(_Float16)1032.f, (_Float16)1032.f};
+        p1 = as_h2((w & 0x00F000F0u) | magic) - h2{(_Float16)1152.f, (_Float16)1152.f};
+        p2 = as_h2((w8 & 0x000F000Fu) | magic) - h2{(_Float16)1032.f, (_Float16)1032.f};
+        p3 = as_h2((w8 & 0x00F000F0u) | magic) - h2{(_Float16)1152.f, (_Float16)1152.f};
     }
-    __device__ static void axpy(const u32x4& w, float ev, float* o) {
+    __device__ static void load_q(QReg& r, const uint16_t* qh, float qs) {
+        r.qs = qs;
+        asm volatile("v_mov_b32 %0, 0x64006400" : "=v"(r.magic));
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {            // q elements 8i..8i+7: 16 bytes
+            const u32x4 w = reinterpret_cast<const u32x4*>(qh)[i];
+            // halves: w.x = (e0, e1), w.y = (e2, e3), w.z = (e4, e5), w.w = (e6, e7)
+            r.q0[i] = as_h2(__builtin_amdgcn_perm(w.z, w.x, 0x05040100u));   // (e0, e4)
+            r.q1[i] = as_h2(__builtin_amdgcn_perm(w.z, w.x, 0x07060302u));   // (e1, e5)
+            r.q2[i] = as_h2(__builtin_amdgcn_perm(w.w, w.y, 0x05040100u));   // (e2, e6)
+            r.q3[i] = as_h2(__builtin_amdgcn_perm(w.w, w.y, 0x07060302u));   // (e3, e7)
+        }
+    }
+    __device__ static float dot(const u32x4& w, const QReg& r) {
+        float a1 = 0.f, a16 = 0.f;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            const uint32_t lo = w[i] & 0x0F0F0F0Fu;
-            const uint32_t hi = (w[i] >> 4) & 0x0F0F0F0Fu;
+            h2 p0, p1, p2, p3;
+            pairs(w[i], r.magic, p0, p1, p2, p3);
+            a1  = __builtin_amdgcn_fdot2(p0, r.q0[i], a1, false);
+            a16 = __builtin_amdgcn_fdot2(p1, r.q1[i], a16, false);
+            a1  = __builtin_amdgcn_fdot2(p2, r.q2[i], a1, false);
+            a16 = __builtin_amdgcn_fdot2(p3, r.q3[i], a16, false);
+        }
+        return __builtin_fmaf(a16, 0.0625f, a1) * r.qs;
+    }
+    __device__ static void axpy(const u32x4& w, float ev, float* o, const QReg& r) {
+        const float ev16 = ev * 0.0625f;
 #pragma unroll
-            for (int b = 0; b < 4; ++b) {
-                o[8 * i + 2 * b]     = __builtin_fmaf(ev, ubyte(lo, b), o[8 * i + 2 * b]);
-                o[8 * i + 2 * b + 1] = __builtin_fmaf(ev, ubyte(hi, b), o[8 * i + 2 * b + 1]);
-            }
+        for (int i = 0; i < 4; ++i) {
+            h2 p0, p1, p2, p3;
+            pairs(w[i], r.magic, p0, p1, p2, p3);
+            o[8 * i + 0] = __builtin_fmaf(ev,   (float)p0.x, o[8 * i + 0]);
+            o[8 * i + 4] = __builtin_fmaf(ev,   (float)p0.y, o[8 * i + 4]);
+            o[8 * i + 1] = __builtin_fmaf(ev16, (float)p1.x, o[8 * i + 1]);
+            o[8 * i + 5] = __builtin_fmaf(ev16, (float)p1.y, o[8 * i + 5]);
+            o[8 * i + 2] = __builtin_fmaf(ev,   (float)p2.x, o[8 * i + 2]);
+            o[8 * i + 6] = __builtin_fmaf(ev,   (float)p2.y, o[8 * i + 6]);
+            o[8 * i + 3] = __builtin_fmaf(ev16, (float)p3.x, o[8 * i + 3]);
+            o[8 * i + 7] = __builtin_fmaf(ev16, (float)p3.y, o[8 * i + 7]);
         }
     }
 };
 
 template <> struct Codec<KQ3> {                  // 32 3-bit fields per lane (v + 4)
     static constexpr int EPL = 32;
-    __device__ static float dot(const u32x3& w, const float* qv) {
+    static constexpr float VBIAS = 4.f;
+    struct QReg { float q[32]; float qbias; };
+    __device__ static void load_q(QReg& r, const uint16_t* qh, float qs) {
+        r.qbias = 0.f;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            const u32x4 w = reinterpret_cast<const u32x4*>(qh)[c];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                r.q[8 * c + 2 * i]     = h2f_lo(w[i]) * qs;
+                r.q[8 * c + 2 * i + 1] = h2f_hi(w[i]) * qs;
+            }
+        }
+#pragma unroll
+        for (int e = 0; e < 32; ++e) r.qbias += r.q[e];
+        r.qbias *= 4.f;
+    }
+    __device__ static float dot(const u32x3& w, const QReg& r) {
         float acc = 0.f;
 #pragma unroll
-        for (int e = 0; e < 32; ++e) acc = __builtin_fmaf((float)field3(w, e), qv[e], acc);
-        return acc;
+        for (int e = 0; e < 32; ++e) acc = __builtin_fmaf((float)field3(w, e), r.q[e], acc);
+        return acc - r.qbias;
     }
-    __device__ static void axpy(const u32x3& w, float ev, float* o) {
+    __device__ static void axpy(const u32x3& w, float ev, float* o, const QReg&) {
 #pragma unroll
         for (int e = 0; e < 32; ++e) o[e] = __builtin_fmaf(ev, (float)field3(w, e), o[e]);
     }
 };
 
 // -------------------------------------------------------- tiled ("+") kernel --
-template <int KIND, int D, int G>
+template <int KIND, int D, int G, int U>
 __global__ __launch_bounds__(256) void decode_tiled(DecodeArgs a) {
     using T = Tile<KIND, D>;
     using C = Codec<KIND>;
@@ -177,14 +361,14 @@ __global__ __launch_bounds__(256) void decode_tiled(DecodeArgs a) {
     constexpr int ROWB = T::ROWB, LB = T::LB, LP = T::LP, PPW = T::PPW, EPL = T::EPL;
     static_assert(EPL == C::EPL, "codec width");
     constexpr bool QUANT = KIND != KF16;
-    constexpr int U   = Unroll<KIND, D>::value;
     constexpr int NG  = D / G;                   // scale groups per row
     constexpr int TW  = PPW * U;                 // rows per wave per iteration
     constexpr int TB  = TW * WAVES;              // rows per work-group per iteration
     constexpr int SCN = QUANT ? TW * NG : 1;     // (k, v) scale pairs per wave tile
-    constexpr int SCL = NG >= 2 ? SCN / 2 : SCN; // lanes that load scales (dwords or halves)
+    constexpr int SCE = !QUANT ? 1 : NG >= 2 ? SCN / 2 : SCN;  // scale dwords/halves per tensor
+    constexpr int SCR = (SCE + 63) / 64;         // scale loads per lane per tensor
     static_assert(!QUANT || G % EPL == 0, "a lane's elements share one scale group");
-    static_assert(SCL <= 64, "one scale load per lane per tensor");
+    static_assert(SCE % 64 == 0 || SCR == 1, "scale entries fill whole wave loads");
 
     __shared__ uint32_t s_scale[WAVES][SCN];
     __shared__ float    s_red[WAVES * 4][D + 1];
@@ -218,48 +402,30 @@ __global__ __launch_bounds__(256) void decode_tiled(DecodeArgs a) {
             rsv = make_rsrc(a.sv + row0 * NG, (uint32_t)n * NG * 2);
         }
 
-        // q slice of this lane, pre-scaled into log2 units.
-        float qv[EPL];
-        {
-            const u32x4* qp = reinterpret_cast<const u32x4*>(a.q + (size_t)h * D + sl * EPL);
-#pragma unroll
-            for (int c = 0; c < EPL / 8; ++c) {
-                const u32x4 w = qp[c];
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    qv[8 * c + 2 * i]     = h2f_lo(w[i]) * a.qscale;
-                    qv[8 * c + 2 * i + 1] = h2f_hi(w[i]) * a.qscale;
-                }
-            }
-        }
-        float qbias = 0.f;
-        if constexpr (QUANT) {
-#pragma unroll
-            for (int e = 0; e < EPL; ++e) qbias += qv[e];
-            qbias *= CodeBias<KIND>::value;
-        }
-
         const uint32_t lane_off = (uint32_t)(pw * ROWB + sl * LB);
         const int niter = (n + TB - 1) / TB;
 
         // Two register stages (A, B) alternate: while one tile is computed the
         // next one is already in flight, and no register copy ever waits on it.
         LoadT ka[U], va_[U], kb[U], vb[U];
-        uint32_t ska = 0, sva = 0, skb = 0, svb = 0;
+        uint32_t ska[SCR], sva[SCR], skb[SCR], svb[SCR];
 
         // Issue order is pinned (scales, then K, then V) so the prologue and the
         // loop leave the same pending-load sequence and the waits stay partial.
-        auto load_tile = [&](int it, LoadT* kk, LoadT* vv, uint32_t& sk, uint32_t& sv) {
+        auto load_tile = [&](int it, LoadT* kk, LoadT* vv, uint32_t* sk, uint32_t* sv) {
             const uint32_t tpos = sgpr((uint32_t)(it * TB + wave * TW));   // wave-uniform
             __builtin_amdgcn_sched_barrier(0);
-            if constexpr (QUANT) {            // lanes >= SCL repeat the last entry (unused)
-                const uint32_t sidx = (uint32_t)min(lane, SCL - 1);
-                if constexpr (NG >= 2) {
-                    sk = ld32(rsk, sidx * 4, tpos * NG * 2);
-                    sv = ld32(rsv, sidx * 4, tpos * NG * 2);
-                } else {
-                    sk = ld16(rsk, sidx * 2, tpos * 2);
-                    sv = ld16(rsv, sidx * 2, tpos * 2);
+            if constexpr (QUANT) {            // lanes past SCE repeat the last entry (unused)
+#pragma unroll
+                for (int r = 0; r < SCR; ++r) {
+                    const uint32_t sidx = (uint32_t)min(lane + 64 * r, SCE - 1);
+                    if constexpr (NG >= 2) {
+                        sk[r] = ld32(rsk, sidx * 4, tpos * NG * 2);
+                        sv[r] = ld32(rsv, sidx * 4, tpos * NG * 2);
+                    } else {
+                        sk[r] = ld16(rsk, sidx * 2, tpos * 2);
+                        sv[r] = ld16(rsv, sidx * 2, tpos * 2);
+                    }
                 }
             }
 #pragma unroll
@@ -271,14 +437,25 @@ __global__ __launch_bounds__(256) void decode_tiled(DecodeArgs a) {
             __builtin_amdgcn_sched_barrier(0);
         };
 
-        auto stage_scales = [&](uint32_t sk, uint32_t sv) {   // (k | v << 16) pairs in LDS
+        // The first tile is issued before q is read, so the two latencies overlap.
+        load_tile(0, ka, va_, ska, sva);
+
+        // q slice of this lane (dims [sl*EPL, sl*EPL + EPL)) in codec form.
+        typename C::QReg qr;
+        C::load_q(qr, a.q + (size_t)h * D + sl * EPL, a.qscale);
+
+        auto stage_scales = [&](const uint32_t* sk, const uint32_t* sv) {  // (k | v << 16) pairs
             if constexpr (QUANT) {
-                if (lane < SCL) {
-                    if constexpr (NG >= 2) {
-                        s_scale[wave][2 * lane]     = __builtin_amdgcn_perm(sv, sk, 0x05040100u);
-                        s_scale[wave][2 * lane + 1] = __builtin_amdgcn_perm(sv, sk, 0x07060302u);
-                    } else {
-                        s_scale[wave][lane] = (sk & 0xFFFFu) | (sv << 16);
+#pragma unroll
+                for (int r = 0; r < SCR; ++r) {
+                    const int e = lane + 64 * r;
+                    if (e < SCE) {
+                        if constexpr (NG >= 2) {
+                            s_scale[wave][2 * e]     = __builtin_amdgcn_perm(sv[r], sk[r], 0x05040100u);
+                            s_scale[wave][2 * e + 1] = __builtin_amdgcn_perm(sv[r], sk[r], 0x07060302u);
+                        } else {
+                            s_scale[wave][e] = (sk[r] & 0xFFFFu) | (sv[r] << 16);
+                        }
                     }
                 }
             }
@@ -291,11 +468,11 @@ __global__ __launch_bounds__(256) void decode_tiled(DecodeArgs a) {
 #pragma unroll
             for (int u = 0; u < U; ++u) {
                 const int slot = u * PPW + pw;
-                float d = C::dot(kk[u], qv);
+                float d = C::dot(kk[u], qr);
                 pair[u] = 0;
                 if constexpr (QUANT) {
                     pair[u] = s_scale[wave][slot * NG + g];
-                    d = (d - qbias) * h2f_lo(pair[u]);
+                    d *= h2f_lo(pair[u]);
                 }
                 d = group_sum<LP>(d);
                 sc[u] = slot < rem ? d : -__builtin_inff();
@@ -317,11 +494,9 @@ __global__ __launch_bounds__(256) void decode_tiled(DecodeArgs a) {
                 const float p = fast_exp2(sc[u] - m);
                 l += p;
                 float ev = p;
-                if constexpr (QUANT) {
-                    ev = p * h2f_hi(pair[u]);
-                    E += ev;
-                }
-                C::axpy(vv[u], ev, o);
+                if constexpr (QUANT) ev = p * h2f_hi(pair[u]);
+                if constexpr (C::VBIAS != 0.f) E += ev;
+                C::axpy(vv[u], ev, o, qr);
             }
         };
 
@@ -330,7 +505,6 @@ __global__ __launch_bounds__(256) void decode_tiled(DecodeArgs a) {
         // prefetch after the last tile and the empty tile that completes an
         // odd count add no traffic and leave (m, l, o) unchanged.
         const int npair = (niter + 1) / 2;
-        load_tile(0, ka, va_, ska, sva);
         for (int ip = 0; ip < npair; ++ip) {
             const int it = 2 * ip;
             stage_scales(ska, sva);
@@ -340,8 +514,8 @@ __global__ __launch_bounds__(256) void decode_tiled(DecodeArgs a) {
             load_tile(it + 2, ka, va_, ska, sva);
             compute_tile(it + 1, kb, vb);
         }
-        if constexpr (QUANT) {
-            const float bias = CodeBias<KIND>::value * E;
+        if constexpr (C::VBIAS != 0.f) {
+            const float bias = C::VBIAS * E;
 #pragma unroll
             for (int e = 0; e < EPL; ++e) o[e] -= bias;
         }
@@ -375,15 +549,16 @@ __global__ __launch_bounds__(256) void decode_tiled(DecodeArgs a) {
 #pragma unroll
         for (int r = 0; r < WAVES * 4; ++r) acc = __builtin_fmaf(f[r / 4], s_red[r][t], acc);
         float* slot = a.ws + (size_t)wg * (D + 2);
-        slot[2 + t] = acc;
+        store_dev(slot + 2 + t, acc);
         if (t == 0) {
             float ls = 0.f;
 #pragma unroll
             for (int r = 0; r < WAVES * 4; ++r) ls = __builtin_fmaf(f[r / 4], s_l[r], ls);
-            slot[0] = M;
-            slot[1] = ls;
+            store_dev(slot, M);
+            store_dev(slot + 1, ls);
         }
     }
+    fused_merge<D>(a, h);
 }
 
 // ------------------------------------------------------- naive (w1) kernel --
@@ -477,15 +652,29 @@ __global__ __launch_bounds__(256) void decode_w1(DecodeArgs a) {
             ls  = __builtin_fmaf(f, s_l[w], ls);
         }
         float* slot = a.ws + (size_t)wg * (D + 2);
-        slot[2 + t] = acc;
-        if (t == 0) { slot[0] = M; slot[1] = ls; }
+        store_dev(slot + 2 + t, acc);
+        if (t == 0) { store_dev(slot, M); store_dev(slot + 1, ls); }
     }
+    fused_merge<D>(a, h);
 }
 
 // ---------------------------------------------------------------- dispatch --
+// Tile depth choice: VA_UNROLL=b in the environment selects the deeper
+// instantiation of every kind (a tuning switch, read once).
+static bool deep_tiles() {
+    static const int v = [] {
+        const char* e = std::getenv("VA_UNROLL");
+        return (e && e[0] == 'b') ? 1 : 0;
+    }();
+    return v != 0;
+}
+
+template <int KIND>
+static int unroll_of() { return deep_tiles() ? UnrollSet<KIND>::b : UnrollSet<KIND>::a; }
+
 template <int KIND, int D>
 static int tiled_positions() {
-    return Tile<KIND, D>::PPW * Unroll<KIND, D>::value * WAVES;
+    return Tile<KIND, D>::PPW * unroll_of<KIND>() * WAVES;
 }
 
 int tile_positions(int kind, bool tiled, int D) {
@@ -502,7 +691,10 @@ template <int KIND, int D, int G>
 static hipError_t launch_one(bool tiled, int H, const DecodeArgs& a, hipStream_t st) {
     const dim3 grid((unsigned)(H * a.S)), block(256);
     if (tiled) {
-        hipLaunchKernelGGL((decode_tiled<KIND, D, G>), grid, block, 0, st, a);
+        if (deep_tiles())
+            hipLaunchKernelGGL((decode_tiled<KIND, D, G, UnrollSet<KIND>::b>), grid, block, 0, st, a);
+        else
+            hipLaunchKernelGGL((decode_tiled<KIND, D, G, UnrollSet<KIND>::a>), grid, block, 0, st, a);
     } else {
         if constexpr (KIND == KQ3) return hipErrorInvalidValue;
         else hipLaunchKernelGGL((decode_w1<KIND, D, G>), grid, block, 0, st, a);

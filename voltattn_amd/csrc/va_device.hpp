@@ -26,14 +26,6 @@ template <int KIND, int D> struct RowBytes {
     static constexpr int value = D * KindBits<KIND>::num / 8;
 };
 
-// Offset added to stored codes to make them unsigned (q8 is stored signed and
-// flipped by xor 0x80; q4 nibbles hold v+8; q3 fields hold v+4).
-template <int KIND> struct CodeBias;
-template <> struct CodeBias<KF16> { static constexpr float value = 0.f; };
-template <> struct CodeBias<KQ8>  { static constexpr float value = 128.f; };
-template <> struct CodeBias<KQ4>  { static constexpr float value = 8.f; };
-template <> struct CodeBias<KQ3>  { static constexpr float value = 4.f; };
-
 // ------------------------------------------------------------ buffer loads --
 // Raw buffer resource: base, no stride, `bytes` records. A load whose offset
 // lies at or beyond `bytes` returns zeros without touching memory, which is
@@ -43,16 +35,23 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, ui
                                              0x00020000);
 }
 
+// Cache policy bits of the streaming K/V loads (gfx950 CPol: 1 = sc0,
+// 2 = nt, 16 = sc1). The K/V stream is read once, so it is loaded
+// non-temporal (nt): measured ~12% faster than the default policy.
+#ifndef VA_LOAD_AUX
+#define VA_LOAD_AUX 2
+#endif
+
 // `soff` must be wave-uniform; it is pinned to an SGPR with readfirstlane so
 // the compiler never wraps the load in a per-lane (waterfall) loop.
 __device__ __forceinline__ uint32_t sgpr(uint32_t x) {
     return (uint32_t)__builtin_amdgcn_readfirstlane((int)x);
 }
 __device__ __forceinline__ u32x4 ld128(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
-    return __builtin_amdgcn_raw_buffer_load_b128(r, voff, sgpr(soff), 0);
+    return __builtin_amdgcn_raw_buffer_load_b128(r, voff, sgpr(soff), VA_LOAD_AUX);
 }
 __device__ __forceinline__ u32x3 ld96(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
-    return __builtin_amdgcn_raw_buffer_load_b96(r, voff, sgpr(soff), 0);
+    return __builtin_amdgcn_raw_buffer_load_b96(r, voff, sgpr(soff), VA_LOAD_AUX);
 }
 __device__ __forceinline__ uint32_t ld32(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
     return __builtin_amdgcn_raw_buffer_load_b32(r, voff, sgpr(soff), 0);
@@ -60,6 +59,21 @@ __device__ __forceinline__ uint32_t ld32(__amdgpu_buffer_rsrc_t r, uint32_t voff
 __device__ __forceinline__ uint32_t ld16(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
     return (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(r, voff, sgpr(soff), 0);
 }
+
+// ------------------------------------------------- device-coherent access --
+// Relaxed device-scope atomic stores/loads compile to global_store/load with
+// sc1: the store is written through to the device coherence point and the
+// load is served from it, so another work-group on any XCD sees the data
+// without an L2 writeback or invalidate (which a device-scope fence would do).
+__device__ __forceinline__ void store_dev(float* p, float v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float load_dev(const float* p) {
+    return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// Wait until every memory operation this wave issued has completed (for the
+// sc1 stores above: reached the coherence point).
+__device__ __forceinline__ void wait_all_mem() { __builtin_amdgcn_s_waitcnt(0); }
 
 // ------------------------------------------------------------------ scalars --
 __device__ __forceinline__ int uniform(int x) { return __builtin_amdgcn_readfirstlane(x); }

@@ -7,6 +7,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <atomic>
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
@@ -82,7 +83,12 @@ int validate(va_fmt fmt, const va_bufs* b, int H, int L, int D, int G, int S, bo
     return VA_OK;
 }
 
-int run_splits(va_fmt fmt, const va_bufs* b, int H, int L, int D, int G, int S, void* stream) {
+std::atomic<unsigned> g_ticket_seq{0};
+
+// fused: merge inside the decode kernel (needs H <= TICKET_MAXH), else the
+// partials are left in ws for a separate merge pass.
+int run_splits(va_fmt fmt, const va_bufs* b, int H, int L, int D, int G, int S, void* stream,
+               bool fused) {
     va::DecodeArgs a;
     a.k  = static_cast<const uint8_t*>(b->k);
     a.v  = static_cast<const uint8_t*>(b->v);
@@ -90,6 +96,8 @@ int run_splits(va_fmt fmt, const va_bufs* b, int H, int L, int D, int G, int S, 
     a.sv = b->sv;
     a.q  = b->q;
     a.ws = b->ws;
+    a.out = b->out;
+    a.ticket_slot = fused ? (int)(g_ticket_seq.fetch_add(1u) % va::TICKET_SLOTS) : -1;
     a.L = L;
     a.S = S;
     a.chunk  = (L + S - 1) / S;
@@ -150,8 +158,11 @@ int va_pick_splits(va_fmt fmt, int H, int L, int D, int* S) {
     if (cus <= 0) cus = 256;
     const int tb    = va::tile_positions(kind_of(fmt), tiled_of(fmt), D);
     const int tiles = (L + tb - 1) / tb;
-    // Aim for ~4 resident work-groups per CU across all heads, whole tiles per split.
-    const int target = std::max(1, (4 * cus + H - 1) / H);
+    // Tiled kernels: ~2 work-groups per CU across all heads (a CU streams at
+    // full rate from two groups; more splits only lengthen the merge). Naive
+    // kernels keep one position per wave in flight, so they need ~8 per CU.
+    const int per_cu = tiled_of(fmt) ? 2 : 8;
+    const int target = std::max(1, (per_cu * cus + H - 1) / H);
     const int s0     = std::max(1, std::min(tiles, target));
     const int tps    = (tiles + s0 - 1) / s0;               // tiles per split
     *S = std::max(1, (L + tps * tb - 1) / (tps * tb));
@@ -161,8 +172,9 @@ int va_pick_splits(va_fmt fmt, int H, int L, int D, int* S) {
 int va_decode(va_fmt fmt, const va_bufs* b, int H, int L, int D, int G, int S, void* stream) {
     int rc = validate(fmt, b, H, L, D, G, S, true);
     if (rc) return rc;
-    rc = run_splits(fmt, b, H, L, D, G, S, stream);
-    if (rc) return rc;
+    const bool fused = H <= va::TICKET_MAXH;
+    rc = run_splits(fmt, b, H, L, D, G, S, stream, fused);
+    if (rc || fused) return rc;
     const hipError_t e = va::launch_merge(b->ws, b->out, H, D, S, as_stream(stream));
     if (e != hipSuccess) return hip_fail(e, "merge launch");
     return VA_OK;
@@ -171,7 +183,7 @@ int va_decode(va_fmt fmt, const va_bufs* b, int H, int L, int D, int G, int S, v
 int va_decode_splits(va_fmt fmt, const va_bufs* b, int H, int L, int D, int G, int S, void* stream) {
     const int rc = validate(fmt, b, H, L, D, G, S, false);
     if (rc) return rc;
-    return run_splits(fmt, b, H, L, D, G, S, stream);
+    return run_splits(fmt, b, H, L, D, G, S, stream, false);
 }
 
 int va_merge(const float* ws, uint16_t* out, int H, int D, int S, void* stream) {
@@ -360,6 +372,32 @@ int va_event_elapsed_ms(void* start, void* stop, float* ms) {
     if (!ms) return fail(VA_ENULL, "ms is NULL");
     VA_HIP(hipEventElapsedTime(ms, static_cast<hipEvent_t>(start), static_cast<hipEvent_t>(stop)),
            "hipEventElapsedTime");
+    return VA_OK;
+}
+
+int va_graph_begin(void* stream) {
+    if (!stream) return fail(VA_EINVAL, "graph capture needs a non-default stream");
+    VA_HIP(hipStreamBeginCapture(as_stream(stream), hipStreamCaptureModeThreadLocal),
+           "hipStreamBeginCapture");
+    return VA_OK;
+}
+int va_graph_end(void* stream, void** graph_exec) {
+    if (!stream || !graph_exec) return fail(VA_ENULL, "stream and graph_exec must be non-NULL");
+    hipGraph_t g = nullptr;
+    VA_HIP(hipStreamEndCapture(as_stream(stream), &g), "hipStreamEndCapture");
+    hipGraphExec_t x = nullptr;
+    const hipError_t e = hipGraphInstantiate(&x, g, nullptr, nullptr, 0);
+    (void)hipGraphDestroy(g);
+    if (e != hipSuccess) return hip_fail(e, "hipGraphInstantiate");
+    *graph_exec = x;
+    return VA_OK;
+}
+int va_graph_launch(void* graph_exec, void* stream) {
+    VA_HIP(hipGraphLaunch(static_cast<hipGraphExec_t>(graph_exec), as_stream(stream)), "hipGraphLaunch");
+    return VA_OK;
+}
+int va_graph_destroy(void* graph_exec) {
+    VA_HIP(hipGraphExecDestroy(static_cast<hipGraphExec_t>(graph_exec)), "hipGraphExecDestroy");
     return VA_OK;
 }
 
