@@ -7,6 +7,7 @@ import numpy as np
 
 import oracle
 import voltattn_amd as va
+from tests.numerics import half_ulp, tight_bound  # noqa: F401 (re-exported)
 
 
 @functools.lru_cache(maxsize=64)
@@ -42,10 +43,3 @@ def run_case(fmt: va.Fmt, c: dict, S: int, splits_only: bool = False) -> dict:
     finally:
         for x in bufs:
             x.free()
-
-
-def half_ulp(x: np.ndarray) -> np.ndarray:
-    """Half the fp16 spacing at |x| (the largest correct-rounding error)."""
-    a = np.abs(np.asarray(x, np.float64)).astype(np.float16)
-    up = np.nextafter(a, np.float16(np.inf)).astype(np.float64) - a.astype(np.float64)
-    return 0.5 * np.maximum(up, 2.0 ** -24)

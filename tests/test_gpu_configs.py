@@ -1,0 +1,98 @@
+"""GPU parity at BASELINE.json's full configuration sizes (H=32, D=128, G=32;
+configs[0]..[4]). Inputs are drawn N(0,1) on the device and quantized there by
+va_quantize (bit-exact with the oracle's quantizer, tests/test_gpu_quantize.py);
+the full decode step runs through the C ABI, and three heads are checked
+exactly: their packed K/V bytes and scales are downloaded, dequantized by the
+oracle and attended in double precision. Checks per head: the reference's gate
+(src/voltattn.cu:903) and the tight per-element bound (tests/numerics.py)."""
+import numpy as np
+import pytest
+
+import oracle
+import voltattn_amd as va
+from tests.numerics import tight_bound
+
+pytestmark = pytest.mark.gpu
+
+H, D = 32, 128
+CONFIGS = [  # (format, L, G)
+    (va.Fmt.Q8, 4096, 32), (va.Fmt.Q8M, 4096, 32),                          # configs[0]
+    (va.Fmt.F16, 16384, 32), (va.Fmt.F16M, 16384, 32),                      # configs[1]
+    (va.Fmt.Q8M, 16384, 32), (va.Fmt.Q8M, 65536, 32),                       # configs[2]
+    (va.Fmt.Q4M, 4096, 32), (va.Fmt.Q4M, 16384, 32), (va.Fmt.Q4M, 65536, 32),  # configs[3]
+    (va.Fmt.Q3M, 65536, 32), (va.Fmt.Q3M, 262144, 32),                      # configs[4]
+    (va.Fmt.Q8M, 16384, 64), (va.Fmt.Q4M, 16384, 64),                       # the reference's G
+    (va.Fmt.Q4, 16384, 32),
+]
+HEADS = (0, 17, 31)
+
+
+def _run_full(fmt, L, G, S=None):
+    bits = va.fmt_bits(fmt)
+    n = H * L * D
+    pay = va.payload_bytes(fmt, H, L, D)
+    sc = va.scale_bytes(fmt, H, L, D, G)
+    S = S or va.pick_splits(fmt, H, L, D)
+    bufs = {}
+    try:
+        for name, size in (("x", n * 4), ("k", pay), ("v", pay), ("q", H * D * 2),
+                           ("out", H * D * 2), ("ws", va.ws_bytes(H, D, S))):
+            bufs[name] = va.DeviceBuffer(size)
+        if sc:
+            bufs["sk"] = va.DeviceBuffer(sc)
+            bufs["sv"] = va.DeviceBuffer(sc)
+        for t, seed in (("k", 101 + L), ("v", 202 + L)):
+            va.fill_normal(bufs["x"].ptr, n, seed)
+            if bits == 16:
+                va.f32_to_f16(bufs["x"].ptr, n, bufs[t].ptr)
+            else:
+                va.quantize(bits, G, bufs["x"].ptr, H * L, D, bufs[t].ptr, bufs["s" + t].ptr)
+        va.fill_normal(bufs["x"].ptr, H * D, 303 + L)
+        va.f32_to_f16(bufs["x"].ptr, H * D, bufs["q"].ptr)
+        va.sync()
+        b = va.DeviceBufs(K=bufs["k"].ptr, V=bufs["v"].ptr, scK=bufs["sk"].ptr if sc else 0,
+                          scV=bufs["sv"].ptr if sc else 0, q=bufs["q"].ptr, out=bufs["out"].ptr,
+                          ws=bufs["ws"].ptr)
+        va.launch(fmt, b, H, L, D, S, G=G)
+        va.sync()
+        out = bufs["out"].download(np.uint16).view(np.float16).astype(np.float64).reshape(H, D)
+        q = bufs["q"].download(np.uint16).reshape(H, D)
+        row = pay // (H * L)
+        heads = {}
+        for h in HEADS:
+            kp = bufs["k"].download(np.uint8, L * row, offset=h * L * row)
+            vp = bufs["v"].download(np.uint8, L * row, offset=h * L * row)
+            if bits == 16:
+                kd = kp.view(np.float16).astype(np.float32)
+                vd = vp.view(np.float16).astype(np.float32)
+            else:
+                ns = L * D // G
+                ks = bufs["sk"].download(np.uint16, ns, offset=h * ns * 2)
+                vs = bufs["sv"].download(np.uint16, ns, offset=h * ns * 2)
+                kd = oracle.dequant(kp, ks, L, D, G, bits)
+                vd = oracle.dequant(vp, vs, L, D, G, bits)
+            heads[h] = oracle.reference(kd, vd, q[h], 1, L, D).astype(np.float64)
+        return out, heads, S
+    finally:
+        for x in bufs.values():
+            x.free()
+
+
+@pytest.mark.parametrize("fmt,L,G", CONFIGS, ids=lambda p: str(p.label if isinstance(p, va.Fmt) else p))
+def test_config_heads_match_oracle(fmt, L, G):
+    print(f"config {fmt.label} H={H} L={L} D={D} G={G}", flush=True)
+    out, heads, S = _run_full(fmt, L, G)
+    assert np.all(np.isfinite(out))
+    for h, ref in heads.items():
+        ok, maxerr = oracle.gate(out[h], ref)
+        assert ok, (h, maxerr)
+        assert np.all(np.abs(out[h] - ref) <= tight_bound(ref)), (h, S)
+
+
+@pytest.mark.parametrize("S", [1, 3, 64, 257])
+def test_split_count_does_not_change_result(S):
+    """Any S (one split per head, odd counts, many short splits) gives the same
+    heads within the tight bound."""
+    out, heads, _ = _run_full(va.Fmt.Q8M, 16384, 32, S=S)
+    for h, ref in heads.items():
+        assert np.all(np.abs(out[h] - ref) <= tight_bound(ref)), (h, S)

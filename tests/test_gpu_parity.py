@@ -48,7 +48,7 @@ def test_selftest_case(param):
     assert np.all(np.isfinite(got))
     assert ok, f"reference gate failed, maxerr={maxerr:.3e}"
     err = np.abs(got.astype(np.float64) - ref)
-    tight = gpu_util.half_ulp(ref) + 2e-6 * np.abs(ref) + 1e-7
+    tight = gpu_util.tight_bound(ref)
     assert np.all(err <= tight), f"tight gate failed at {np.argmax(err - tight)}"
     if G == 64:
         logged = LOGGED[(fmt.label, H, L, D, S)]

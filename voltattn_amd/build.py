@@ -90,7 +90,7 @@ def build_cli() -> Path:
     tmp = out.with_name("voltattn.tmp")
     _run([
         "g++", "-O2", "-std=c++17", "-Wall", "-Wextra", "-Werror", "-pthread",
-        "-I", str(ROOT / "include"), "-I", str(ROOT / "oracle"),
+        "-I", str(ROOT / "include"), "-I", str(ROOT / "oracle"), "-I", str(PKG / "host"),
         str(ROOT / "tests" / "cli" / "voltattn_cli.cpp"),
         "-o", str(tmp),
         f"-L{PKG}", "-lvoltattn_hip", f"-Wl,-rpath,{PKG}", f"-Wl,-rpath,$ORIGIN/../voltattn_amd",

@@ -23,11 +23,9 @@
 // stay <= 2^RESCALE_SLACK and most tiles skip the rescale entirely. (o, l, m)
 // always describe the same normalised value, so the result is unchanged.
 //
-// q8 and q3 codes are consumed unsigned (q8 xor 0x80, q3 field) with one
-// convert each; their constant offset is removed once: from the score via the
-// lane's sum of q, and from o via the running sum of the weights (E). q4 codes
-// become exact fp16 values two at a time and feed v_dot2_f32_f16 (K) and
-// v_fma_mix_f32 (V); see Codec<KQ4>.
+// Codes become exact fp16 values two at a time with bit operations and feed
+// v_dot2_f32_f16 / v_fma_mix_f32 directly (see the lane codecs), so no
+// separate convert or offset correction runs per element.
 //
 // Naive kernels (f16, q8, q4): one wave64 per position, D/64 elements per
 // lane, a 6-step cross-lane sum and an exact per-position online-softmax
@@ -37,6 +35,7 @@
 #include "va_kernels.hpp"
 
 #include <cstdlib>
+#include <utility>
 
 namespace va {
 
@@ -159,136 +158,142 @@ lane_load(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
     else return ld128(r, voff, soff);
 }
 
-__device__ __forceinline__ float ubyte(uint32_t w, int b) {
-    return (float)((w >> (8 * b)) & 0xFFu);              // v_cvt_f32_ubyte{b}
-}
-
-// 3-bit field e (0..31) of a 96-bit little-endian lane word.
-__device__ __forceinline__ uint32_t field3(const u32x3& w, int e) {
-    const int b = 3 * e;
-    if (b + 3 <= 32) return (w.x >> b) & 7u;
-    if (b < 32)      return __builtin_amdgcn_alignbit(w.y, w.x, b) & 7u;
-    if (b + 3 <= 64) return (w.y >> (b - 32)) & 7u;
-    if (b < 64)      return __builtin_amdgcn_alignbit(w.z, w.y, b - 32) & 7u;
-    return (w.z >> (b - 64)) & 7u;
-}
-
-// Per-kind lane codec over the EPL elements a lane owns in one row:
-//   QReg       the lane's slice of q in the form the codec consumes;
-//   load_q     q (fp16, 16-byte aligned lane slice) -> QReg; qs = log2(e)/sqrt(D);
-//   dot        sum_e q_e * code_e in log2 units (q pre-scaled), any code offset removed;
-//   axpy       o_e += ev * code_e (code still offset by VBIAS, if nonzero);
-//   VBIAS      offset left in the V codes; the kernel removes VBIAS * sum(ev) once.
+// ------------------------------------------------------------ lane codecs --
+// A lane owns EPL consecutive elements of a row. Every codec turns the stored
+// codes into exact fp16 values two at a time (bit ops only), so the arithmetic
+// sees exactly the dequantized integers:
+//   * K: v_dot2_f32_f16 against the unscaled fp16 q (f16, q8, q4: products of
+//     two fp16 values are exact in fp32), or v_fma_mix_f32 against fp32 q (q3);
+//   * V: v_fma_mix_f32, o_e += ev * code_e with an fp16 operand and fp32
+//     accumulation (P.V stays fp32).
+// The fp16 "magic" construction: OR-ing a code n (< 2^10 / 2^r) shifted left by
+// r into the mantissa of 1024.0 (0x6400) gives 1024 + 2^r n exactly; one packed
+// fp16 subtract of 1024 + 2^r * offset then leaves 2^r * v. The magic constant
+// lives in a VGPR so mask-and-insert is one v_and_or_b32 (a gfx9 VOP3 reads one
+// scalar constant; mask and magic cannot both be literals).
+//
+// Interface: QReg (the lane's q in codec form), load_q(QReg&, q slice, qs) with
+// qs = log2(e)/sqrt(D), dot(w, QReg) -> q.k in log2 units, axpy(w, ev, o, QReg),
+// finish(o) (per-element fix-up once at the end).
 typedef _Float16 h2 __attribute__((ext_vector_type(2)));
 __device__ __forceinline__ h2 as_h2(uint32_t x) { return __builtin_bit_cast(h2, x); }
+__device__ __forceinline__ h2 hh(float a, float b) { return h2{(_Float16)a, (_Float16)b}; }
+
+#define VA_VGPR_CONST(dst, imm) asm volatile("v_mov_b32 %0, " #imm : "=v"(dst))
+
+// Load a lane's q slice (EPL fp16 values, 16-byte aligned) as raw dwords.
+template <int EPL>
+__device__ __forceinline__ void load_q_words(uint32_t (&qw)[EPL / 2], const uint16_t* qh) {
+#pragma unroll
+    for (int c = 0; c < EPL / 8; ++c) {
+        const u32x4 w = reinterpret_cast<const u32x4*>(qh)[c];
+        qw[4 * c] = w.x; qw[4 * c + 1] = w.y; qw[4 * c + 2] = w.z; qw[4 * c + 3] = w.w;
+    }
+}
 
 template <int KIND> struct Codec;
 
-template <> struct Codec<KF16> {                 // 8 halves per lane
+// f16: 8 halves per lane, element 2i+j in half j of dword i.
+template <> struct Codec<KF16> {
     static constexpr int EPL = 8;
-    static constexpr float VBIAS = 0.f;
-    struct QReg { float q[8]; };
+    struct QReg { h2 q[4]; float qs; };
     __device__ static void load_q(QReg& r, const uint16_t* qh, float qs) {
-        const u32x4 w = *reinterpret_cast<const u32x4*>(qh);
+        uint32_t qw[4];
+        load_q_words<8>(qw, qh);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            r.q[2 * i]     = h2f_lo(w[i]) * qs;
-            r.q[2 * i + 1] = h2f_hi(w[i]) * qs;
-        }
+        for (int i = 0; i < 4; ++i) r.q[i] = as_h2(qw[i]);
+        r.qs = qs;
     }
     __device__ static float dot(const u32x4& w, const QReg& r) {
-        float acc = 0.f;
+        float a = 0.f;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            acc = __builtin_fmaf(h2f_lo(w[i]), r.q[2 * i], acc);
-            acc = __builtin_fmaf(h2f_hi(w[i]), r.q[2 * i + 1], acc);
-        }
-        return acc;
+        for (int i = 0; i < 4; ++i) a = __builtin_amdgcn_fdot2(as_h2(w[i]), r.q[i], a, false);
+        return a * r.qs;
     }
     __device__ static void axpy(const u32x4& w, float ev, float* o, const QReg&) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            o[2 * i]     = __builtin_fmaf(ev, h2f_lo(w[i]), o[2 * i]);
-            o[2 * i + 1] = __builtin_fmaf(ev, h2f_hi(w[i]), o[2 * i + 1]);
+            const h2 v = as_h2(w[i]);
+            o[2 * i]     = __builtin_fmaf(ev, (float)v.x, o[2 * i]);
+            o[2 * i + 1] = __builtin_fmaf(ev, (float)v.y, o[2 * i + 1]);
         }
     }
+    __device__ static void finish(float*) {}
 };
 
-template <> struct Codec<KQ8> {                  // 16 int8 per lane, consumed as u8 = v + 128
+// q8: 16 int8 per lane, element 4i+b in byte b of dword i. xor 0x80 makes the
+// bytes u = v + 128; v_perm_b32 places bytes (b0, b1) / (b2, b3) under the
+// 0x64 magic byte: fp16 pair (1024 + u, 1024 + u'), minus 1152 -> (v, v').
+template <> struct Codec<KQ8> {
     static constexpr int EPL = 16;
-    static constexpr float VBIAS = 128.f;
-    struct QReg { float q[16]; float qbias; };
+    struct QReg { h2 q[8]; float qs; uint32_t magic; };
+    __device__ static void pairs(uint32_t w, uint32_t magic, h2& p01, h2& p23) {
+        const uint32_t u = w ^ 0x80808080u;
+        p01 = as_h2(__builtin_amdgcn_perm(magic, u, 0x04010400u)) - hh(1152.f, 1152.f);
+        p23 = as_h2(__builtin_amdgcn_perm(magic, u, 0x04030402u)) - hh(1152.f, 1152.f);
+    }
     __device__ static void load_q(QReg& r, const uint16_t* qh, float qs) {
-        r.qbias = 0.f;
+        uint32_t qw[8];
+        load_q_words<16>(qw, qh);
 #pragma unroll
-        for (int c = 0; c < 2; ++c) {
-            const u32x4 w = reinterpret_cast<const u32x4*>(qh)[c];
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                r.q[8 * c + 2 * i]     = h2f_lo(w[i]) * qs;
-                r.q[8 * c + 2 * i + 1] = h2f_hi(w[i]) * qs;
-            }
-        }
-#pragma unroll
-        for (int e = 0; e < 16; ++e) r.qbias += r.q[e];
-        r.qbias *= 128.f;
+        for (int i = 0; i < 8; ++i) r.q[i] = as_h2(qw[i]);
+        r.qs = qs;
+        VA_VGPR_CONST(r.magic, 0x64646464);
     }
     __device__ static float dot(const u32x4& w, const QReg& r) {
-        float acc = 0.f;
+        float a = 0.f;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            const uint32_t u = w[i] ^ 0x80808080u;
-#pragma unroll
-            for (int b = 0; b < 4; ++b) acc = __builtin_fmaf(ubyte(u, b), r.q[4 * i + b], acc);
+            h2 p01, p23;
+            pairs(w[i], r.magic, p01, p23);
+            a = __builtin_amdgcn_fdot2(p01, r.q[2 * i], a, false);
+            a = __builtin_amdgcn_fdot2(p23, r.q[2 * i + 1], a, false);
         }
-        return acc - r.qbias;
+        return a * r.qs;
     }
-    __device__ static void axpy(const u32x4& w, float ev, float* o, const QReg&) {
+    __device__ static void axpy(const u32x4& w, float ev, float* o, const QReg& r) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            const uint32_t u = w[i] ^ 0x80808080u;
-#pragma unroll
-            for (int b = 0; b < 4; ++b)
-                o[4 * i + b] = __builtin_fmaf(ev, ubyte(u, b), o[4 * i + b]);
+            h2 p01, p23;
+            pairs(w[i], r.magic, p01, p23);
+            o[4 * i + 0] = __builtin_fmaf(ev, (float)p01.x, o[4 * i + 0]);
+            o[4 * i + 1] = __builtin_fmaf(ev, (float)p01.y, o[4 * i + 1]);
+            o[4 * i + 2] = __builtin_fmaf(ev, (float)p23.x, o[4 * i + 2]);
+            o[4 * i + 3] = __builtin_fmaf(ev, (float)p23.y, o[4 * i + 3]);
         }
     }
+    __device__ static void finish(float*) {}
 };
 
-// q4: 32 nibbles per lane; element 8i+j of the lane sits in nibble j of dword i.
-// Each dword becomes four exact fp16 pairs: OR-ing a nibble into the mantissa
-// of 1024.0 (0x6400) gives 1024 + n (or 1024 + 16n for a high nibble left in
-// place), and one packed subtract of 1032 (1152) leaves v = n - 8 (16v):
-//   P0 = (e0, e4) = v,  P1 = (e1, e5) = 16v,  P2 = (e2, e6) = v,  P3 = (e3, e7) = 16v
-// (P2/P3 from the dword shifted right by 8). Every value is an exact small
-// integer, so K is consumed by v_dot2_f32_f16 against the unscaled fp16 q
-// (exact products, fp32 accumulation; the 16v pairs in a second accumulator
-// scaled by 1/16 at the end) and V by v_fma_mix_f32 (fp16 operand, fp32 FMA).
+// q4: 32 nibbles per lane; element 8i+j sits in nibble j of dword i. Masking
+// nibbles (0, 4) / (1, 5) in place and (2, 6) / (3, 7) after a shift by 8 under
+// the 1024.0 magic gives the exact pairs
+//   P0 = (e0, e4) = v,  P1 = (e1, e5) = 16v,  P2 = (e2, e6) = v,  P3 = (e3, e7) = 16v;
+// the 16v pairs accumulate separately (scaled by 1/16 once) for K and use
+// ev/16 for V.
 template <> struct Codec<KQ4> {
     static constexpr int EPL = 32;
-    static constexpr float VBIAS = 0.f;
-    // magic: 0x64006400 held in a VGPR, so the mask-and-insert is one
-    // v_and_or_b32 (a gfx9 VOP3 takes one scalar constant; mask and magic
-    // cannot both be literals).
     struct QReg { h2 q0[4], q1[4], q2[4], q3[4]; float qs; uint32_t magic; };
     __device__ static void pairs(uint32_t w, uint32_t magic, h2& p0, h2& p1, h2& p2, h2& p3) {
         const uint32_t w8 = w >> 8;
-        p0 = as_h2((w & 0x000F000Fu) | magic) - h2{(_Float16)1032.f, (_Float16)1032.f};
-        p1 = as_h2((w & 0x00F000F0u) | magic) - h2{(_Float16)1152.f, (_Float16)1152.f};
-        p2 = as_h2((w8 & 0x000F000Fu) | magic) - h2{(_Float16)1032.f, (_Float16)1032.f};
-        p3 = as_h2((w8 & 0x00F000F0u) | magic) - h2{(_Float16)1152.f, (_Float16)1152.f};
+        p0 = as_h2((w & 0x000F000Fu) | magic) - hh(1032.f, 1032.f);
+        p1 = as_h2((w & 0x00F000F0u) | magic) - hh(1152.f, 1152.f);
+        p2 = as_h2((w8 & 0x000F000Fu) | magic) - hh(1032.f, 1032.f);
+        p3 = as_h2((w8 & 0x00F000F0u) | magic) - hh(1152.f, 1152.f);
     }
     __device__ static void load_q(QReg& r, const uint16_t* qh, float qs) {
-        r.qs = qs;
-        asm volatile("v_mov_b32 %0, 0x64006400" : "=v"(r.magic));
+        uint32_t qw[16];
+        load_q_words<32>(qw, qh);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {            // q elements 8i..8i+7: 16 bytes
-            const u32x4 w = reinterpret_cast<const u32x4*>(qh)[i];
-            // halves: w.x = (e0, e1), w.y = (e2, e3), w.z = (e4, e5), w.w = (e6, e7)
-            r.q0[i] = as_h2(__builtin_amdgcn_perm(w.z, w.x, 0x05040100u));   // (e0, e4)
-            r.q1[i] = as_h2(__builtin_amdgcn_perm(w.z, w.x, 0x07060302u));   // (e1, e5)
-            r.q2[i] = as_h2(__builtin_amdgcn_perm(w.w, w.y, 0x05040100u));   // (e2, e6)
-            r.q3[i] = as_h2(__builtin_amdgcn_perm(w.w, w.y, 0x07060302u));   // (e3, e7)
+        for (int i = 0; i < 4; ++i) {
+            // halves of elements 8i..8i+7: qw[4i] = (e0, e1), +1 = (e2, e3), +2 = (e4, e5), +3 = (e6, e7)
+            r.q0[i] = as_h2(__builtin_amdgcn_perm(qw[4 * i + 2], qw[4 * i], 0x05040100u));      // (e0, e4)
+            r.q1[i] = as_h2(__builtin_amdgcn_perm(qw[4 * i + 2], qw[4 * i], 0x07060302u));      // (e1, e5)
+            r.q2[i] = as_h2(__builtin_amdgcn_perm(qw[4 * i + 3], qw[4 * i + 1], 0x05040100u));  // (e2, e6)
+            r.q3[i] = as_h2(__builtin_amdgcn_perm(qw[4 * i + 3], qw[4 * i + 1], 0x07060302u));  // (e3, e7)
         }
+        r.qs = qs;
+        VA_VGPR_CONST(r.magic, 0x64006400);
     }
     __device__ static float dot(const u32x4& w, const QReg& r) {
         float a1 = 0.f, a16 = 0.f;
@@ -319,36 +324,91 @@ template <> struct Codec<KQ4> {
             o[8 * i + 7] = __builtin_fmaf(ev16, (float)p3.y, o[8 * i + 7]);
         }
     }
+    __device__ static void finish(float*) {}
 };
 
-template <> struct Codec<KQ3> {                  // 32 3-bit fields per lane (v + 4)
+// q3: 32 3-bit fields per lane, element e at bits [3e, 3e+3) of the lane's
+// 96-bit little-endian word (v + 4). Eight 32-bit windows of that word (one
+// alignbit/shift each) hold two pairs apiece: a field at bit r of the low half
+// and one at bit 16 + r' of the high half, r, r' <= 7. The 16 pairs:
+//   window s = 0, 6, 12, 36, 42, 48: (a, a+6) at (0, 18) and (a+1, a+7) at (3, 21), a = s/3
+//   window s = 68, 74:               (a, a+4) at (4, 16) and (a+1, a+5) at (7, 19), a = (s+4)/3
+// A pair becomes (2^r v, 2^r' v') exactly; K uses fp32 q pre-scaled by 2^-r,
+// V accumulates 2^r v and finish() scales o_e by 2^-r once.
+struct Q3Pair { int a, b, s, r, rp; };
+__device__ constexpr Q3Pair kQ3Pairs[16] = {
+    {0, 6, 0, 0, 2},    {1, 7, 0, 3, 5},    {2, 8, 6, 0, 2},    {3, 9, 6, 3, 5},
+    {4, 10, 12, 0, 2},  {5, 11, 12, 3, 5},  {12, 18, 36, 0, 2}, {13, 19, 36, 3, 5},
+    {14, 20, 42, 0, 2}, {15, 21, 42, 3, 5}, {16, 22, 48, 0, 2}, {17, 23, 48, 3, 5},
+    {24, 28, 68, 4, 0}, {25, 29, 68, 7, 3}, {26, 30, 74, 4, 0}, {27, 31, 74, 7, 3},
+};
+__device__ constexpr int q3_shift(int e) {          // r of element e in its pair
+    for (int i = 0; i < 16; ++i) {
+        if (kQ3Pairs[i].a == e) return kQ3Pairs[i].r;
+        if (kQ3Pairs[i].b == e) return kQ3Pairs[i].rp;
+    }
+    return 0;
+}
+
+template <> struct Codec<KQ3> {
     static constexpr int EPL = 32;
-    static constexpr float VBIAS = 4.f;
-    struct QReg { float q[32]; float qbias; };
+    struct QReg { float q[32]; uint32_t magic; };
+    __device__ static uint32_t window(const u32x3& w, int s) {
+        if (s == 0) return w.x;
+        if (s < 32) return __builtin_amdgcn_alignbit(w.y, w.x, s);
+        if (s == 32) return w.y;
+        if (s < 64) return __builtin_amdgcn_alignbit(w.z, w.y, s - 32);
+        return w.z >> (s - 64);
+    }
+    template <int I>
+    __device__ static h2 pair(const u32x3& w, uint32_t magic) {
+        constexpr Q3Pair P = kQ3Pairs[I];
+        constexpr uint32_t mask = (7u << P.r) | (7u << (16 + P.rp));
+        return as_h2((window(w, P.s) & mask) | magic) -
+               hh(1024.f + 4.f * (float)(1 << P.r), 1024.f + 4.f * (float)(1 << P.rp));
+    }
     __device__ static void load_q(QReg& r, const uint16_t* qh, float qs) {
-        r.qbias = 0.f;
+        uint32_t qw[16];
+        load_q_words<32>(qw, qh);
 #pragma unroll
-        for (int c = 0; c < 4; ++c) {
-            const u32x4 w = reinterpret_cast<const u32x4*>(qh)[c];
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                r.q[8 * c + 2 * i]     = h2f_lo(w[i]) * qs;
-                r.q[8 * c + 2 * i + 1] = h2f_hi(w[i]) * qs;
-            }
+        for (int e = 0; e < 32; ++e) {
+            const float x = (e & 1) ? h2f_hi(qw[e / 2]) : h2f_lo(qw[e / 2]);
+            r.q[e] = x * qs * (1.0f / (float)(1 << q3_shift(e)));
         }
-#pragma unroll
-        for (int e = 0; e < 32; ++e) r.qbias += r.q[e];
-        r.qbias *= 4.f;
+        VA_VGPR_CONST(r.magic, 0x64006400);
+    }
+    template <int I>
+    __device__ static void dot_pair(const u32x3& w, const QReg& r, float& a) {
+        const h2 p = pair<I>(w, r.magic);
+        a = __builtin_fmaf((float)p.x, r.q[kQ3Pairs[I].a], a);
+        a = __builtin_fmaf((float)p.y, r.q[kQ3Pairs[I].b], a);
+    }
+    template <int I>
+    __device__ static void axpy_pair(const u32x3& w, float ev, float* o, const QReg& r) {
+        const h2 p = pair<I>(w, r.magic);
+        o[kQ3Pairs[I].a] = __builtin_fmaf(ev, (float)p.x, o[kQ3Pairs[I].a]);
+        o[kQ3Pairs[I].b] = __builtin_fmaf(ev, (float)p.y, o[kQ3Pairs[I].b]);
+    }
+    template <int... I>
+    __device__ static float dot_all(const u32x3& w, const QReg& r, std::integer_sequence<int, I...>) {
+        float a0 = 0.f, a1 = 0.f;
+        ((I % 2 ? dot_pair<I>(w, r, a1) : dot_pair<I>(w, r, a0)), ...);
+        return a0 + a1;
+    }
+    template <int... I>
+    __device__ static void axpy_all(const u32x3& w, float ev, float* o, const QReg& r,
+                                    std::integer_sequence<int, I...>) {
+        (axpy_pair<I>(w, ev, o, r), ...);
     }
     __device__ static float dot(const u32x3& w, const QReg& r) {
-        float acc = 0.f;
-#pragma unroll
-        for (int e = 0; e < 32; ++e) acc = __builtin_fmaf((float)field3(w, e), r.q[e], acc);
-        return acc - r.qbias;
+        return dot_all(w, r, std::make_integer_sequence<int, 16>{});
     }
-    __device__ static void axpy(const u32x3& w, float ev, float* o, const QReg&) {
+    __device__ static void axpy(const u32x3& w, float ev, float* o, const QReg& r) {
+        axpy_all(w, ev, o, r, std::make_integer_sequence<int, 16>{});
+    }
+    __device__ static void finish(float* o) {
 #pragma unroll
-        for (int e = 0; e < 32; ++e) o[e] = __builtin_fmaf(ev, (float)field3(w, e), o[e]);
+        for (int e = 0; e < 32; ++e) o[e] *= 1.0f / (float)(1 << q3_shift(e));
     }
 };
 
@@ -387,7 +447,7 @@ __global__ __launch_bounds__(256) void decode_tiled(DecodeArgs a) {
     const int j0 = s * a.chunk;
     const int n  = min(a.L - j0, a.chunk);       // rows of this split (<= 0: empty)
 
-    float m = M_INIT, l = 0.f, E = 0.f;
+    float m = M_INIT, l = 0.f;
     float o[EPL];
 #pragma unroll
     for (int e = 0; e < EPL; ++e) o[e] = 0.f;
@@ -484,7 +544,6 @@ __global__ __launch_bounds__(256) void decode_tiled(DecodeArgs a) {
                 const float mn = uniformf(wave_max(fmaxf(m, tmax)));
                 const float c  = fast_exp2(m - mn);
                 l *= c;
-                E *= c;
 #pragma unroll
                 for (int e = 0; e < EPL; ++e) o[e] *= c;
                 m = mn;
@@ -495,7 +554,6 @@ __global__ __launch_bounds__(256) void decode_tiled(DecodeArgs a) {
                 l += p;
                 float ev = p;
                 if constexpr (QUANT) ev = p * h2f_hi(pair[u]);
-                if constexpr (C::VBIAS != 0.f) E += ev;
                 C::axpy(vv[u], ev, o, qr);
             }
         };
@@ -514,11 +572,7 @@ __global__ __launch_bounds__(256) void decode_tiled(DecodeArgs a) {
             load_tile(it + 2, ka, va_, ska, sva);
             compute_tile(it + 1, kb, vb);
         }
-        if constexpr (C::VBIAS != 0.f) {
-            const float bias = C::VBIAS * E;
-#pragma unroll
-            for (int e = 0; e < EPL; ++e) o[e] -= bias;
-        }
+        C::finish(o);
     }
 
     // ---- work-group merge: slots of a DPP row first, then rows/waves via LDS.
