@@ -197,13 +197,15 @@ def cpu_baseline(H, L, D, G) -> dict:
 
 
 def load_traffic(name: str):
+    """HBM bytes per decode launch measured by rocprofv3 FETCH_SIZE + WRITE_SIZE
+    (calibrated against a copy of known size), committed in profiles/traffic.json
+    by the profiling runs that profiles/*_hbm_traffic.md documents; None if absent."""
     p = ROOT / "profiles" / "traffic.json"
-    if p.exists():
-        try:
-            return json.loads(p.read_text()).get(name)
-        except (ValueError, OSError):
-            return None
-    return None
+    try:
+        entry = json.loads(p.read_text()).get(name)
+    except (ValueError, OSError):
+        return None
+    return None if entry is None else float(entry["traffic_bytes"])
 
 
 def main() -> int:
@@ -221,6 +223,9 @@ def main() -> int:
     ap.add_argument("--probe-gib", type=float, default=4.0)
     ap.add_argument("--set-gib", type=float, default=2.0, help="rotated working set per format")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--copy-probe-mib", type=int, default=0,
+                    help="first run one plain device-to-device copy of this many MiB "
+                         "(calibrates rocprof FETCH_SIZE/WRITE_SIZE against known bytes)")
     args = ap.parse_args()
 
     if args.gpus != 1:
@@ -237,6 +242,19 @@ def main() -> int:
         f"mem={info['total_mem'] / 2**30:.0f} GiB")
     ceiling = va.probe_read(int(args.probe_gib * 2**30), reps=5)
     log(f"probed read ceiling: {ceiling:.1f} GB/s ({args.probe_gib:g} GiB buffer)")
+
+    if args.copy_probe_mib > 0:
+        nb = args.copy_probe_mib << 20
+        src, dst = va.DeviceBuffer(nb), va.DeviceBuffer(nb)
+        try:
+            va.fill_normal(src.ptr, nb // 4, 7)
+            va.sync()
+            va.check(va.lib.va_memcpy_d2d(dst.ptr, src.ptr, nb, None))
+            va.sync()
+        finally:
+            src.free()
+            dst.free()
+        log(f"copy probe: {nb} bytes device-to-device")
 
     H, L, D, G = args.H, args.L, args.D, args.G
     stream = va.Stream()
