@@ -1,7 +1,7 @@
 // va_runtime.hip — the C ABI (include/voltattn.h): argument validation,
 // format -> kernel dispatch, and the thin HIP runtime shims the host harness
 // uses. This is the only translation unit that calls the HIP runtime API.
-#include "../../include/voltattn.h"
+#include "voltattn.h"
 #include "va_kernels.hpp"
 
 #include <hip/hip_runtime.h>
