@@ -42,92 +42,145 @@ namespace va {
 constexpr int WAVES = 4;                 // waves per work-group
 constexpr float RESCALE_SLACK = 8.0f;    // log2 units: weights stay <= 256
 constexpr float M_INIT = -1e30f;         // finite "no score yet" maximum
-constexpr float M_FLOOR = -3.0e38f;      // below every partial's m
 
-// Arrival counters of the fused merge (zero-initialised with the code object).
+// Ticket lines and partial store of the fused merge (zero-initialised with
+// the code object; layout in va_kernels.hpp).
 __device__ __align__(256) unsigned g_tickets[TICKET_SLOTS * TICKET_MAXH * TICKET_STRIDE];
+__device__ __align__(256) uint64_t g_parts[(size_t)TICKET_SLOTS * PART_CAP * PART_STRIDE];
 
-// Log-sum-exp merge of one head's S partials by a whole work-group (256
-// threads): thread (d, sg) folds splits sg, sg + 256/D, ... with a running
-// maximum, eight loads in flight per round; the split groups are then combined
-// through LDS. Same algebra as the standalone merge pass (va_merge.hip).
-template <int D>
-__device__ void block_merge(const float* __restrict__ base, int S, uint16_t* __restrict__ outh) {
-    constexpr int NSG = 256 / D;
-    constexpr int PT  = 8;
-    __shared__ float s_acc[NSG][D];
-    __shared__ float s_lg[NSG];
-    __shared__ float s_mw[WAVES];
-    const int t = (int)threadIdx.x, d = t % D, sg = t / D;
-    const size_t stride = (size_t)(D + 2);
-    float mt = M_FLOOR, acc = 0.f, lacc = 0.f;
-    for (int s0 = sg; s0 < S; s0 += NSG * PT) {
-        float mv[PT], lv[PT], ov[PT];
-#pragma unroll
-        for (int i = 0; i < PT; ++i) {
-            const int s = s0 + NSG * i;
-            const bool ok = s < S;
-            const float* slot = base + (size_t)(ok ? s : 0) * stride;
-            mv[i] = ok ? load_dev(slot) : M_FLOOR;
-            lv[i] = ok ? load_dev(slot + 1) : 0.f;
-            ov[i] = ok ? load_dev(slot + 2 + d) : 0.f;
-        }
-        float mr = mt;
-#pragma unroll
-        for (int i = 0; i < PT; ++i) mr = fmaxf(mr, mv[i]);
-        const float c = fast_exp2(mt - mr);
-        acc *= c;
-        lacc *= c;
-#pragma unroll
-        for (int i = 0; i < PT; ++i) {
-            const float w = fast_exp2(mv[i] - mr);
-            acc  = __builtin_fmaf(w, ov[i], acc);
-            lacc = __builtin_fmaf(w, lv[i], lacc);
-        }
-        mt = mr;
+constexpr int POLL_MAX    = 1 << 12;     // bound on re-reads of one in-flight word
+
+__device__ __forceinline__ uint64_t tagged(float v, uint32_t tag) {
+    return ((uint64_t)tag << 32) | __builtin_bit_cast(uint32_t, v);
+}
+__device__ __forceinline__ bool tag_ok(uint64_t w, uint32_t tag) { return (uint32_t)(w >> 32) == tag; }
+__device__ __forceinline__ float tag_val(uint64_t w) { return __builtin_bit_cast(float, (uint32_t)w); }
+
+// Re-read the word at p until it carries `tag` (bounded); returns the last read.
+__device__ __noinline__ uint64_t poll_word(const uint64_t* p, uint32_t tag) {
+    uint64_t w = load_dev(p);
+    for (int k = 0; k < POLL_MAX && !tag_ok(w, tag); ++k) {
+        __builtin_amdgcn_s_sleep(2);
+        w = load_dev(p);
     }
-    const float wm = wave_max(mt);
-    if ((t & 63) == 0) s_mw[t >> 6] = wm;
-    __syncthreads();
-    float M = s_mw[0];
-#pragma unroll
-    for (int w = 1; w < WAVES; ++w) M = fmaxf(M, s_mw[w]);
-    const float f = fast_exp2(mt - M);
-    s_acc[sg][d] = acc * f;
-    if (d == 0) s_lg[sg] = lacc * f;
-    __syncthreads();
-    if (t < D) {
-        float o = 0.f, l = 0.f;
-#pragma unroll
-        for (int g = 0; g < NSG; ++g) {
-            o += s_acc[g][t];
-            l += s_lg[g];
-        }
-        outh[t] = f2h_rne(o / l);
-    }
+    return w;
 }
 
-// Fused second pass: after a work-group has written its partial, the group
-// that completes head h (the S-th arrival on the head's counter) merges all S
-// partials and resets the counter. Partials are stored and loaded with
-// device-scope coherent accesses (store_dev/load_dev), and every thread waits
-// for its stores to complete before the barrier that precedes the ticket
-// increment, so the merging group reads every partial from the coherence
-// point without any L2 writeback or invalidate.
-template <int D>
-__device__ void fused_merge(const DecodeArgs& a, int h) {
-    if (a.ticket_slot < 0) return;
+// The call epoch of head h on this call's ticket slot; read at kernel start
+// (the merge of this call advances it only after every group has arrived).
+__device__ __forceinline__ unsigned read_epoch(const DecodeArgs& a, int h) {
+    if (a.ticket_slot < 0) return 0u;
+    return load_dev(g_tickets + ((size_t)a.ticket_slot * TICKET_MAXH + h) * TICKET_STRIDE + 1);
+}
+
+// End of a work-group (head h, split s): thread t < D holds o[t] = acc of the
+// group's partial (m, l, o), and each such thread also holds m and l.
+//
+// Two-pass form (ticket_slot < 0): the partial goes to ws for the merge pass.
+//
+// Fused form: every value of the partial is stored as one 64-bit word
+// (tag << 32 | fp32 bits), tag = (epoch << 9 | h << 1 | 1), unique per head
+// and call and never zero. Thread 255 (which stores nothing, so its wait
+// covers only its own atomic) takes the head's ticket right after the group's
+// barrier, without waiting for the stores to complete; the group that
+// completes the ticket merges. It uses its own partial from registers and
+// reads the others; a word whose tag is stale belongs to a group that has
+// already arrived and issued its stores, so it is re-read (bounded) until it
+// lands. Each wave holding o columns merges on its own: lane j takes split
+// j's (m, l), the maximum and the l sum are wave reductions in a fixed order,
+// and o[t] folds the splits in order with lane j's weight read by readlane,
+// so the result does not depend on arrival order. Needs S <= 64. CH o values
+// are loaded per round (the naive kernels use fewer to keep their occupancy).
+template <int D, int CH>
+__device__ void finish_partial(const DecodeArgs& a, int h, int s, float M, float ls, float acc,
+                               unsigned epoch) {
+    const int t = (int)threadIdx.x;
+    if (a.ticket_slot < 0) {
+        if (t < D) {
+            float* slot = a.ws + ((size_t)h * a.S + s) * (D + 2);
+            store_dev(slot + 2 + t, acc);
+            if (t == 0) {
+                store_dev(slot, M);
+                store_dev(slot + 1, ls);
+            }
+        }
+        return;
+    }
     __shared__ int s_last;
-    wait_all_mem();
-    __syncthreads();
     unsigned* ticket = g_tickets + ((size_t)a.ticket_slot * TICKET_MAXH + h) * TICKET_STRIDE;
-    if (threadIdx.x == 0)
+    if (t == 255)
         s_last = __hip_atomic_fetch_add(ticket, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
                  (unsigned)(a.S - 1);
+    const uint32_t tag = (epoch << 9) | ((uint32_t)h << 1) | 1u;
+    const uint64_t* part = g_parts + ((size_t)a.ticket_slot * PART_CAP + (size_t)h * a.S) * PART_STRIDE;
+    if (t < D) {
+        uint64_t* mine = const_cast<uint64_t*>(part) + (size_t)s * PART_STRIDE;
+        store_dev(mine + 2 + t, tagged(acc, tag));
+        if (t == 0) {
+            store_dev(mine, tagged(M, tag));
+            store_dev(mine + 1, tagged(ls, tag));
+        }
+    }
     __syncthreads();
-    if (!s_last) return;
-    block_merge<D>(a.ws + (size_t)h * a.S * (D + 2), a.S, a.out + (size_t)h * D);
-    if (threadIdx.x == 0) __hip_atomic_store(ticket, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (!s_last || t >= D) return;
+
+    // Loads are unconditional (indexes clamped into this head's partials) and
+    // values are selected afterwards, so every load of a round is in flight
+    // at once; the first o round is issued together with (m, l).
+    const int lane = t & 63;
+    const float NEG = -__builtin_inff();
+    const uint64_t* pl = part + (size_t)min(lane, a.S - 1) * PART_STRIDE;
+    uint64_t wm = load_dev(pl), wl = load_dev(pl + 1);
+    uint64_t wo[CH];
+    auto load_chunk = [&](int c0) {
+#pragma unroll
+        for (int i = 0; i < CH; ++i) {
+            const int j = c0 + i;
+            const uint64_t w = load_dev(part + (size_t)min(j, a.S - 1) * PART_STRIDE + 2 + t);
+            wo[i] = (j < a.S && j != s) ? w : tagged(j == s ? acc : 0.f, tag);
+        }
+    };
+    load_chunk(0);
+    if (lane == s) { wm = tagged(M, tag); wl = tagged(ls, tag); }
+    if (lane >= a.S) { wm = tagged(NEG, tag); wl = tagged(0.f, tag); }
+    bool good = true;
+    if (!(tag_ok(wm, tag) && tag_ok(wl, tag))) {     // rare: stores still in flight
+        wm = tag_ok(wm, tag) ? wm : poll_word(pl, tag);
+        wl = tag_ok(wl, tag) ? wl : poll_word(pl + 1, tag);
+        good = tag_ok(wm, tag) && tag_ok(wl, tag);
+    }
+    const float mx = wave_max(tag_val(wm));
+    const float wj = fast_exp2(tag_val(wm) - mx);     // weight of split `lane` (0 past S)
+    const float lsum = wave_sum(wj * tag_val(wl));
+    float o = 0.f;
+    for (int c0 = 0; c0 < a.S; c0 += CH) {
+        if (c0 > 0) load_chunk(c0);
+        bool ok = true;
+#pragma unroll
+        for (int i = 0; i < CH; ++i) ok = ok && tag_ok(wo[i], tag);
+        if (!ok) {
+#pragma unroll
+            for (int i = 0; i < CH; ++i) {
+                if (!tag_ok(wo[i], tag)) {
+                    wo[i] = poll_word(part + (size_t)(c0 + i) * PART_STRIDE + 2 + t, tag);
+                    good = good && tag_ok(wo[i], tag);
+                }
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < CH; ++i) {
+            const float w = __builtin_bit_cast(float,
+                __builtin_amdgcn_readlane(__builtin_bit_cast(int, wj), c0 + i));
+            o = __builtin_fmaf(w, tag_val(wo[i]), o);
+        }
+    }
+    // A lost partial (never observed within the poll bound) shows as NaN.
+    good = __builtin_amdgcn_ballot_w64(!good) == 0;
+    a.out[(size_t)h * D + t] = good ? f2h_rne(o / lsum) : (uint16_t)0x7E00u;
+    if (t == 0) {                            // every arrival is in: reset for the slot's next call
+        store_dev(ticket, 0u);
+        store_dev(ticket + 1, epoch + 1u);
+    }
 }
 
 // --------------------------------------------------------------- layouts ----
@@ -438,6 +491,7 @@ __global__ __launch_bounds__(256) void decode_tiled(DecodeArgs a) {
     const int wg   = blockIdx.x;
     const int h    = wg / a.S;
     const int s    = wg - h * a.S;
+    const unsigned epoch = read_epoch(a, h);
     const int wave = uniform((int)(threadIdx.x >> 6));
     const int lane = (int)(threadIdx.x & 63);
     const int sl   = lane % LP;                  // lane within its row
@@ -592,27 +646,20 @@ __global__ __launch_bounds__(256) void decode_tiled(DecodeArgs a) {
     if (lane == 0) s_m[wave] = m;
     __syncthreads();
     const int t = (int)threadIdx.x;
+    float M = 0.f, acc = 0.f, ls = 0.f;
     if (t < D) {
-        float M = s_m[0];
+        M = s_m[0];
 #pragma unroll
         for (int w = 1; w < WAVES; ++w) M = fmaxf(M, s_m[w]);
         float f[WAVES];
 #pragma unroll
         for (int w = 0; w < WAVES; ++w) f[w] = fast_exp2(s_m[w] - M);
-        float acc = 0.f;
 #pragma unroll
         for (int r = 0; r < WAVES * 4; ++r) acc = __builtin_fmaf(f[r / 4], s_red[r][t], acc);
-        float* slot = a.ws + (size_t)wg * (D + 2);
-        store_dev(slot + 2 + t, acc);
-        if (t == 0) {
-            float ls = 0.f;
 #pragma unroll
-            for (int r = 0; r < WAVES * 4; ++r) ls = __builtin_fmaf(f[r / 4], s_l[r], ls);
-            store_dev(slot, M);
-            store_dev(slot + 1, ls);
-        }
+        for (int r = 0; r < WAVES * 4; ++r) ls = __builtin_fmaf(f[r / 4], s_l[r], ls);
     }
-    fused_merge<D>(a, h);
+    finish_partial<D, 16>(a, h, s, M, ls, acc, epoch);
 }
 
 // ------------------------------------------------------- naive (w1) kernel --
@@ -631,6 +678,7 @@ __global__ __launch_bounds__(256) void decode_w1(DecodeArgs a) {
     const int wg   = blockIdx.x;
     const int h    = wg / a.S;
     const int s    = wg - h * a.S;
+    const unsigned epoch = read_epoch(a, h);
     const int wave = (int)(threadIdx.x >> 6);
     const int lane = (int)(threadIdx.x & 63);
     const int g    = (lane * P) / G;
@@ -694,22 +742,19 @@ __global__ __launch_bounds__(256) void decode_w1(DecodeArgs a) {
     if (lane == 0) { s_m[wave] = m; s_l[wave] = l; }
     __syncthreads();
     const int t = (int)threadIdx.x;
+    float M = 0.f, acc = 0.f, ls = 0.f;
     if (t < D) {
-        float M = s_m[0];
+        M = s_m[0];
 #pragma unroll
         for (int w = 1; w < WAVES; ++w) M = fmaxf(M, s_m[w]);
-        float acc = 0.f, ls = 0.f;
 #pragma unroll
         for (int w = 0; w < WAVES; ++w) {
             const float f = fast_exp2(s_m[w] - M);
             acc = __builtin_fmaf(f, s_o[w][t], acc);
             ls  = __builtin_fmaf(f, s_l[w], ls);
         }
-        float* slot = a.ws + (size_t)wg * (D + 2);
-        store_dev(slot + 2 + t, acc);
-        if (t == 0) { store_dev(slot, M); store_dev(slot + 1, ls); }
     }
-    fused_merge<D>(a, h);
+    finish_partial<D, 8>(a, h, s, M, ls, acc, epoch);
 }
 
 // ---------------------------------------------------------------- dispatch --

@@ -15,21 +15,27 @@ struct DecodeArgs {
     const uint16_t* sv;
     const uint16_t* q;      // fp16 [H][D]
     float*          ws;     // [H*S][D+2]: (m, l, o[D]) per split, m in log2 units
+                            // (two-pass form only)
     uint16_t*       out;    // fp16 [H][D], written by the fused merge
     int   L, S, chunk;
     float qscale;           // log2(e) / sqrt(D)
-    int   ticket_slot;      // >= 0: fused merge on this ticket slot; < 0: partials only
+    int   ticket_slot;      // >= 0: fused merge on this ticket slot; < 0: partials to ws
 };
 
-// Fused second pass: per-head arrival counters in static device memory
-// (zero at load, reset by the merging work-group). Calls rotate over
-// TICKET_SLOTS slots, so up to that many decode calls may be in flight on one
-// device at once; more than TICKET_MAXH heads use the separate merge kernel.
-// Each counter sits alone in a 256-byte line: atomics to one line serialize
-// at the memory side, and the S arrivals of every head land together.
+// Fused second pass: per-(slot, head) ticket lines in static device memory
+// (zero at load): word 0 counts the arrivals of the head's work-groups, word 1
+// is the head's call epoch, advanced by the merging work-group. Calls rotate
+// over TICKET_SLOTS slots, so up to that many decode calls may be in flight on
+// one device at once. Each line is 256 bytes: atomics to one line serialize at
+// the memory side, and the S arrivals of every head land together.
+// The partials of a fused call live in library memory (PART_CAP partials of
+// PART_STRIDE 64-bit words per slot), not in the caller's ws. Calls with more
+// than TICKET_MAXH heads or more than PART_CAP partials use the two-pass form.
 constexpr int TICKET_SLOTS  = 16;
 constexpr int TICKET_MAXH   = 256;
-constexpr int TICKET_STRIDE = 64;   // uint32 per counter (256 bytes)
+constexpr int TICKET_STRIDE = 64;   // uint32 per ticket line (256 bytes)
+constexpr int PART_CAP      = 1024; // partials (H*S) per slot
+constexpr int PART_STRIDE   = 130;  // 64-bit words per partial: m, l, o[D], D <= 128
 
 // kind: 0 f16, 1 q8, 2 q4, 3 q3. tiled: the "+" kernels; otherwise the naive
 // one-position-per-wave kernels (f16, q8, q4 only).

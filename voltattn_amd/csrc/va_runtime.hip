@@ -85,8 +85,8 @@ int validate(va_fmt fmt, const va_bufs* b, int H, int L, int D, int G, int S, bo
 
 std::atomic<unsigned> g_ticket_seq{0};
 
-// fused: merge inside the decode kernel (needs H <= TICKET_MAXH), else the
-// partials are left in ws for a separate merge pass.
+// fused: merge inside the decode kernel (needs H <= TICKET_MAXH, S <= 64 and
+// H*S <= PART_CAP), else the partials are left in ws for a separate merge pass.
 int run_splits(va_fmt fmt, const va_bufs* b, int H, int L, int D, int G, int S, void* stream,
                bool fused) {
     va::DecodeArgs a;
@@ -172,7 +172,7 @@ int va_pick_splits(va_fmt fmt, int H, int L, int D, int* S) {
 int va_decode(va_fmt fmt, const va_bufs* b, int H, int L, int D, int G, int S, void* stream) {
     int rc = validate(fmt, b, H, L, D, G, S, true);
     if (rc) return rc;
-    const bool fused = H <= va::TICKET_MAXH;
+    const bool fused = H <= va::TICKET_MAXH && S <= 64 && (long long)H * S <= va::PART_CAP;
     rc = run_splits(fmt, b, H, L, D, G, S, stream, fused);
     if (rc || fused) return rc;
     const hipError_t e = va::launch_merge(b->ws, b->out, H, D, S, as_stream(stream));
