@@ -154,6 +154,7 @@ Row bench_one(Fmt f, int H, int L, int D, int G, int reps, double set_bytes, voi
                              q.as<uint16_t>(), out.as<uint16_t>(), ws.as<float>()};
     }
     auto step = [&](int i) { launch(f, bufs[i % copies], H, L, D, S, G, stream); };
+    for (int c = 0; c < copies; ++c) step(c);               // residency pass: every copy touched once
     for (int w = 0; w < 3; ++w) step(w);                    // src/voltattn.cu:1038
     check(va_stream_sync(stream));
     Event e0, e1;

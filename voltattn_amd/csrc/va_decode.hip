@@ -34,6 +34,7 @@
 #include "va_device.hpp"
 #include "va_kernels.hpp"
 
+#include <algorithm>
 #include <cstdlib>
 #include <utility>
 
@@ -91,7 +92,7 @@ __device__ __forceinline__ unsigned read_epoch(const DecodeArgs& a, int h) {
 // and o[t] folds the splits in order with lane j's weight read by readlane,
 // so the result does not depend on arrival order. Needs S <= 64. CH o values
 // are loaded per round (the naive kernels use fewer to keep their occupancy).
-template <int D, int CH>
+template <int D, int CH, int NT>
 __device__ void finish_partial(const DecodeArgs& a, int h, int s, float M, float ls, float acc,
                                unsigned epoch) {
     const int t = (int)threadIdx.x;
@@ -108,7 +109,7 @@ __device__ void finish_partial(const DecodeArgs& a, int h, int s, float M, float
     }
     __shared__ int s_last;
     unsigned* ticket = g_tickets + ((size_t)a.ticket_slot * TICKET_MAXH + h) * TICKET_STRIDE;
-    if (t == 255)
+    if (t == NT - 1)
         s_last = __hip_atomic_fetch_add(ticket, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
                  (unsigned)(a.S - 1);
     const uint32_t tag = (epoch << 9) | ((uint32_t)h << 1) | 1u;
@@ -194,7 +195,7 @@ template <int KIND, int D> struct Tile {
 };
 
 // Rows per lane per tile and tensor (U). Each kind is instantiated for two
-// depths; va_unroll() picks one at run time (default: the first).
+// depths; the dispatch below picks one per kind.
 template <int KIND> struct UnrollSet;
 template <> struct UnrollSet<KF16> { static constexpr int a = 4, b = 8; };
 template <> struct UnrollSet<KQ8>  { static constexpr int a = 2, b = 4; };
@@ -466,8 +467,8 @@ template <> struct Codec<KQ3> {
 };
 
 // -------------------------------------------------------- tiled ("+") kernel --
-template <int KIND, int D, int G, int U>
-__global__ __launch_bounds__(256) void decode_tiled(DecodeArgs a) {
+template <int KIND, int D, int G, int U, int WAVES>
+__global__ __launch_bounds__(WAVES * 64) void decode_tiled(DecodeArgs a) {
     using T = Tile<KIND, D>;
     using C = Codec<KIND>;
     using LoadT = typename LaneLoad<KIND>::type;
@@ -659,7 +660,7 @@ __global__ __launch_bounds__(256) void decode_tiled(DecodeArgs a) {
 #pragma unroll
         for (int r = 0; r < WAVES * 4; ++r) ls = __builtin_fmaf(f[r / 4], s_l[r], ls);
     }
-    finish_partial<D, 16>(a, h, s, M, ls, acc, epoch);
+    finish_partial<D, 16, WAVES * 64>(a, h, s, M, ls, acc, epoch);
 }
 
 // ------------------------------------------------------- naive (w1) kernel --
@@ -754,46 +755,83 @@ __global__ __launch_bounds__(256) void decode_w1(DecodeArgs a) {
             ls  = __builtin_fmaf(f, s_l[w], ls);
         }
     }
-    finish_partial<D, 8>(a, h, s, M, ls, acc, epoch);
+    finish_partial<D, 8, WAVES * 64>(a, h, s, M, ls, acc, epoch);
 }
 
 // ---------------------------------------------------------------- dispatch --
-// Tile depth choice: VA_UNROLL=b in the environment selects the deeper
-// instantiation of every kind (a tuning switch, read once).
-static bool deep_tiles() {
-    static const int v = [] {
-        const char* e = std::getenv("VA_UNROLL");
-        return (e && e[0] == 'b') ? 1 : 0;
-    }();
-    return v != 0;
+// Tiled configuration per kind: waves per group and tile depth (UnrollSet a or
+// b), measured at H=32 D=128 over L = 4K..64K on MI355X. Every default keeps
+// the same bytes in flight per CU (8 waves x depth a); fewer, deeper groups
+// mean fewer partials to merge and a shorter dispatch. VA_WAVES=4|8 and
+// VA_UNROLL=a|b in the environment override the defaults (tuning switches,
+// read once).
+struct TiledCfg { int waves; bool deep; };
+
+static TiledCfg default_cfg(int kind) {
+    switch (kind) {
+        case KF16: return {8, false};    // 8 waves x 4 rows
+        case KQ8:  return {4, true};     // 4 waves x 4 rows
+        case KQ4:  return {4, true};     // 4 waves x 4 rows
+        default:   return {4, false};    // q3: 4 waves x 2 rows, two groups per CU
+    }
+}
+
+static TiledCfg tiled_cfg(int kind) {
+    static const int w = [] { const char* e = std::getenv("VA_WAVES");  return e ? e[0] : 0; }();
+    static const int u = [] { const char* e = std::getenv("VA_UNROLL"); return e ? e[0] : 0; }();
+    TiledCfg c = default_cfg(kind);
+    if (w == '4' || w == '8') c.waves = w - '0';
+    if (u == 'a' || u == 'b') c.deep = u == 'b';
+    return c;
+}
+
+template <int KIND> static int unroll_of(bool deep) { return deep ? UnrollSet<KIND>::b : UnrollSet<KIND>::a; }
+
+template <int KIND, int D>
+static int tiled_positions(const TiledCfg& c) {
+    return Tile<KIND, D>::PPW * unroll_of<KIND>(c.deep) * c.waves;
 }
 
 template <int KIND>
-static int unroll_of() { return deep_tiles() ? UnrollSet<KIND>::b : UnrollSet<KIND>::a; }
-
-template <int KIND, int D>
-static int tiled_positions() {
-    return Tile<KIND, D>::PPW * unroll_of<KIND>() * WAVES;
+static int tiled_groups(const TiledCfg& c) {
+    return std::max(1, 8 * UnrollSet<KIND>::a / (c.waves * unroll_of<KIND>(c.deep)));
 }
 
 int tile_positions(int kind, bool tiled, int D) {
     if (!tiled) return WAVES;
+    const TiledCfg c = tiled_cfg(kind);
     switch (kind) {
-        case KF16: return D == 128 ? tiled_positions<KF16, 128>() : tiled_positions<KF16, 64>();
-        case KQ8:  return D == 128 ? tiled_positions<KQ8, 128>()  : tiled_positions<KQ8, 64>();
-        case KQ4:  return D == 128 ? tiled_positions<KQ4, 128>()  : tiled_positions<KQ4, 64>();
-        default:   return D == 128 ? tiled_positions<KQ3, 128>()  : tiled_positions<KQ3, 64>();
+        case KF16: return D == 128 ? tiled_positions<KF16, 128>(c) : tiled_positions<KF16, 64>(c);
+        case KQ8:  return D == 128 ? tiled_positions<KQ8, 128>(c)  : tiled_positions<KQ8, 64>(c);
+        case KQ4:  return D == 128 ? tiled_positions<KQ4, 128>(c)  : tiled_positions<KQ4, 64>(c);
+        default:   return D == 128 ? tiled_positions<KQ3, 128>(c)  : tiled_positions<KQ3, 64>(c);
+    }
+}
+
+int groups_per_cu(int kind, bool tiled) {
+    if (!tiled) return 8;                 // naive: one position per wave, 32 waves per CU
+    const TiledCfg c = tiled_cfg(kind);
+    switch (kind) {
+        case KF16: return tiled_groups<KF16>(c);
+        case KQ8:  return tiled_groups<KQ8>(c);
+        case KQ4:  return tiled_groups<KQ4>(c);
+        default:   return tiled_groups<KQ3>(c);
     }
 }
 
 template <int KIND, int D, int G>
 static hipError_t launch_one(bool tiled, int H, const DecodeArgs& a, hipStream_t st) {
-    const dim3 grid((unsigned)(H * a.S)), block(256);
+    const dim3 grid((unsigned)(H * a.S)), block(256), block8(512);
     if (tiled) {
-        if (deep_tiles())
-            hipLaunchKernelGGL((decode_tiled<KIND, D, G, UnrollSet<KIND>::b>), grid, block, 0, st, a);
-        else
-            hipLaunchKernelGGL((decode_tiled<KIND, D, G, UnrollSet<KIND>::a>), grid, block, 0, st, a);
+        constexpr int UA = UnrollSet<KIND>::a, UB = UnrollSet<KIND>::b;
+        const TiledCfg c = tiled_cfg(KIND);
+        if (c.waves == 8) {
+            if (c.deep) hipLaunchKernelGGL((decode_tiled<KIND, D, G, UB, 8>), grid, block8, 0, st, a);
+            else        hipLaunchKernelGGL((decode_tiled<KIND, D, G, UA, 8>), grid, block8, 0, st, a);
+        } else {
+            if (c.deep) hipLaunchKernelGGL((decode_tiled<KIND, D, G, UB, 4>), grid, block, 0, st, a);
+            else        hipLaunchKernelGGL((decode_tiled<KIND, D, G, UA, 4>), grid, block, 0, st, a);
+        }
     } else {
         if constexpr (KIND == KQ3) return hipErrorInvalidValue;
         else hipLaunchKernelGGL((decode_w1<KIND, D, G>), grid, block, 0, st, a);

@@ -42,6 +42,10 @@ constexpr int PART_STRIDE   = 130;  // 64-bit words per partial: m, l, o[D], D <
 hipError_t launch_decode(int kind, bool tiled, int H, int D, int G,
                          const DecodeArgs& a, hipStream_t stream);
 
+// Work-groups per CU the split rule aims for (tiled kernels: the configured
+// groups per CU of the kind; naive kernels: 8).
+int groups_per_cu(int kind, bool tiled);
+
 // Positions one work-group of the tiled kernel covers per loop iteration;
 // split lengths that are multiples of it leave no partial tile.
 int tile_positions(int kind, bool tiled, int D);

@@ -158,10 +158,10 @@ int va_pick_splits(va_fmt fmt, int H, int L, int D, int* S) {
     if (cus <= 0) cus = 256;
     const int tb    = va::tile_positions(kind_of(fmt), tiled_of(fmt), D);
     const int tiles = (L + tb - 1) / tb;
-    // Tiled kernels: ~2 work-groups per CU across all heads (a CU streams at
-    // full rate from two groups; more splits only lengthen the merge). Naive
+    // Tiled kernels: the kind's configured groups per CU (one or two groups
+    // stream a CU at full rate; more splits only lengthen the merge). Naive
     // kernels keep one position per wave in flight, so they need ~8 per CU.
-    const int per_cu = tiled_of(fmt) ? 2 : 8;
+    const int per_cu = va::groups_per_cu(kind_of(fmt), tiled_of(fmt));
     const int target = std::max(1, (per_cu * cus + H - 1) / H);
     const int s0     = std::max(1, std::min(tiles, target));
     const int tps    = (tiles + s0 - 1) / s0;               // tiles per split
