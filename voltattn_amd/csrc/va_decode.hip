@@ -57,14 +57,11 @@ __device__ __forceinline__ uint64_t tagged(float v, uint32_t tag) {
 __device__ __forceinline__ bool tag_ok(uint64_t w, uint32_t tag) { return (uint32_t)(w >> 32) == tag; }
 __device__ __forceinline__ float tag_val(uint64_t w) { return __builtin_bit_cast(float, (uint32_t)w); }
 
-// Re-read the word at p until it carries `tag` (bounded); returns the last read.
-__device__ __noinline__ uint64_t poll_word(const uint64_t* p, uint32_t tag) {
-    uint64_t w = load_dev(p);
-    for (int k = 0; k < POLL_MAX && !tag_ok(w, tag); ++k) {
-        __builtin_amdgcn_s_sleep(2);
-        w = load_dev(p);
-    }
-    return w;
+// 16 bytes (two tagged words) from the device coherence point (sc1, as the
+// relaxed agent-scope loads above). The compiler tracks these like any buffer
+// load, so a round of them is in flight at once.
+__device__ __forceinline__ u32x4 ld128_dev(__amdgpu_buffer_rsrc_t r, uint32_t voff) {
+    return __builtin_amdgcn_raw_buffer_load_b128(r, voff, 0, 16 /* sc1 */);
 }
 
 // The call epoch of head h on this call's ticket slot; read at kernel start
@@ -74,27 +71,36 @@ __device__ __forceinline__ unsigned read_epoch(const DecodeArgs& a, int h) {
     return load_dev(g_tickets + ((size_t)a.ticket_slot * TICKET_MAXH + h) * TICKET_STRIDE + 1);
 }
 
-// End of a work-group (head h, split s): thread t < D holds o[t] = acc of the
-// group's partial (m, l, o), and each such thread also holds m and l.
+// End of a work-group (head h, split s) of NT threads: thread t < D holds
+// o[t] = acc of the group's partial (m, l, o), and each such thread also holds
+// m and l.
 //
 // Two-pass form (ticket_slot < 0): the partial goes to ws for the merge pass.
 //
 // Fused form: every value of the partial is stored as one 64-bit word
 // (tag << 32 | fp32 bits), tag = (epoch << 9 | h << 1 | 1), unique per head
-// and call and never zero. Thread 255 (which stores nothing, so its wait
-// covers only its own atomic) takes the head's ticket right after the group's
-// barrier, without waiting for the stores to complete; the group that
-// completes the ticket merges. It uses its own partial from registers and
-// reads the others; a word whose tag is stale belongs to a group that has
-// already arrived and issued its stores, so it is re-read (bounded) until it
-// lands. Each wave holding o columns merges on its own: lane j takes split
-// j's (m, l), the maximum and the l sum are wave reductions in a fixed order,
-// and o[t] folds the splits in order with lane j's weight read by readlane,
-// so the result does not depend on arrival order. Needs S <= 64. CH o values
-// are loaded per round (the naive kernels use fewer to keep their occupancy).
-template <int D, int CH, int NT>
+// and call and never zero; a partial is PART_STRIDE words: m, l, o[0..D).
+// Thread NT-1 (which stores nothing, so its wait covers only its own atomic)
+// takes the head's ticket without waiting for the stores to complete; the
+// group that completes the ticket merges. It keeps its own partial in LDS and
+// reads the others with 16-byte coherent loads, each carrying two words; a
+// word whose tag is stale belongs to a group that has already arrived and
+// issued its stores, so it is re-read (bounded) until it lands.
+//
+// The merge spreads the loads over all NT/64 waves, so each wave issues only
+// 1 + ceil(S / (NT/64)) loads (coherent loads are serviced one instruction at
+// a time): lane j of every wave reads split j's (m, l); wave w folds splits
+// j = w, w + NW, ... in increasing order into lane-pair columns (2i, 2i+1)
+// with split j's weight read by readlane; the NW wave sums are added in wave
+// order through LDS. The order is fixed, so the result does not depend on
+// arrival order. Needs S <= 64.
+template <int D, int NT>
 __device__ void finish_partial(const DecodeArgs& a, int h, int s, float M, float ls, float acc,
                                unsigned epoch) {
+    constexpr int NW = NT / 64;
+    constexpr int R  = 4;                       // o-pair loads per wave per round
+    constexpr uint32_t PB = PART_STRIDE * 8;    // bytes per partial (16-byte multiple)
+    static_assert(PB % 16 == 0 && D + 2 <= PART_STRIDE, "partial layout");
     const int t = (int)threadIdx.x;
     if (a.ticket_slot < 0) {
         if (t < D) {
@@ -107,77 +113,121 @@ __device__ void finish_partial(const DecodeArgs& a, int h, int s, float M, float
         }
         return;
     }
-    __shared__ int s_last;
+    __shared__ int   s_last, s_bad;
+    __shared__ float s_own[D + 2];              // o[0..D), m, l of this group
+    __shared__ float s_fold[NW][D];
     unsigned* ticket = g_tickets + ((size_t)a.ticket_slot * TICKET_MAXH + h) * TICKET_STRIDE;
     if (t == NT - 1)
         s_last = __hip_atomic_fetch_add(ticket, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
                  (unsigned)(a.S - 1);
     const uint32_t tag = (epoch << 9) | ((uint32_t)h << 1) | 1u;
-    const uint64_t* part = g_parts + ((size_t)a.ticket_slot * PART_CAP + (size_t)h * a.S) * PART_STRIDE;
+    uint64_t* part = g_parts + ((size_t)a.ticket_slot * PART_CAP + (size_t)h * a.S) * PART_STRIDE;
     if (t < D) {
-        uint64_t* mine = const_cast<uint64_t*>(part) + (size_t)s * PART_STRIDE;
+        uint64_t* mine = part + (size_t)s * PART_STRIDE;
         store_dev(mine + 2 + t, tagged(acc, tag));
+        s_own[t] = acc;
         if (t == 0) {
             store_dev(mine, tagged(M, tag));
             store_dev(mine + 1, tagged(ls, tag));
+            s_own[D] = M;
+            s_own[D + 1] = ls;
+            s_bad = 0;
         }
     }
     __syncthreads();
-    if (!s_last || t >= D) return;
+    if (!s_last) return;
 
-    // Loads are unconditional (indexes clamped into this head's partials) and
-    // values are selected afterwards, so every load of a round is in flight
-    // at once; the first o round is issued together with (m, l).
+    const int w    = uniform(t >> 6);
     const int lane = t & 63;
-    const float NEG = -__builtin_inff();
-    const uint64_t* pl = part + (size_t)min(lane, a.S - 1) * PART_STRIDE;
-    uint64_t wm = load_dev(pl), wl = load_dev(pl + 1);
-    uint64_t wo[CH];
-    auto load_chunk = [&](int c0) {
+    const int dp   = min(lane, D / 2 - 1);     // o pair of this lane: dims 2dp, 2dp + 1
+    const __amdgpu_buffer_rsrc_t rp = make_rsrc(part, (uint32_t)a.S * PB);
+    bool good;
+
+    // (m, l) of split `lane` (words 0, 1 of its partial).
+    const int jl = min(lane, a.S - 1);
+    u32x4 ml = ld128_dev(rp, (uint32_t)jl * PB);
+    // First round of this wave's o pairs, issued together with (m, l).
+    u32x4 op[R];
+    auto load_round = [&](int j0) {
 #pragma unroll
-        for (int i = 0; i < CH; ++i) {
-            const int j = c0 + i;
-            const uint64_t w = load_dev(part + (size_t)min(j, a.S - 1) * PART_STRIDE + 2 + t);
-            wo[i] = (j < a.S && j != s) ? w : tagged(j == s ? acc : 0.f, tag);
+        for (int i = 0; i < R; ++i) {
+            const int j = j0 + NW * i;           // wave-uniform: no load past the last split
+            if (j < a.S) op[i] = ld128_dev(rp, (uint32_t)j * PB + 16u + (uint32_t)dp * 16u);
         }
     };
-    load_chunk(0);
-    if (lane == s) { wm = tagged(M, tag); wl = tagged(ls, tag); }
-    if (lane >= a.S) { wm = tagged(NEG, tag); wl = tagged(0.f, tag); }
-    bool good = true;
-    if (!(tag_ok(wm, tag) && tag_ok(wl, tag))) {     // rare: stores still in flight
-        wm = tag_ok(wm, tag) ? wm : poll_word(pl, tag);
-        wl = tag_ok(wl, tag) ? wl : poll_word(pl + 1, tag);
-        good = tag_ok(wm, tag) && tag_ok(wl, tag);
+    load_round(w);
+    // Selection is branch-free and the rare re-read loop is wave-uniform (all
+    // lanes run it, stale lanes take the new value), so no loaded value has to
+    // survive a divergent branch.
+    // The words are taken out of the vector right after each load (the
+    // compiler mis-tracked a 16-byte value carried through the re-read loop).
+    const bool in_s = lane < a.S, own = lane == s;
+    uint32_t mv = ml.x, mt = ml.y, lv = ml.z, lt = ml.w;
+    for (int k = 0; k < POLL_MAX; ++k) {          // rare: stores still in flight
+        const bool need = in_s && !own && !(mt == tag && lt == tag);
+        if (__builtin_amdgcn_ballot_w64(need) == 0) break;
+        __builtin_amdgcn_s_sleep(2);
+        const u32x4 re = ld128_dev(rp, (uint32_t)jl * PB);
+        const uint32_t rmv = re.x, rmt = re.y, rlv = re.z, rlt = re.w;
+        mv = need ? rmv : mv;
+        mt = need ? rmt : mt;
+        lv = need ? rlv : lv;
+        lt = need ? rlt : lt;
     }
-    const float mx = wave_max(tag_val(wm));
-    const float wj = fast_exp2(tag_val(wm) - mx);     // weight of split `lane` (0 past S)
-    const float lsum = wave_sum(wj * tag_val(wl));
-    float o = 0.f;
-    for (int c0 = 0; c0 < a.S; c0 += CH) {
-        if (c0 > 0) load_chunk(c0);
-        bool ok = true;
+    good = !in_s || own || (mt == tag && lt == tag);
+    const float own_m = s_own[D], own_l = s_own[D + 1];
+    const float mj = !in_s ? -__builtin_inff() : own ? own_m : __builtin_bit_cast(float, mv);
+    const float lj = !in_s ? 0.f : own ? own_l : __builtin_bit_cast(float, lv);
+    const float mx   = wave_max(mj);
+    const float wj   = fast_exp2(mj - mx);      // weight of split `lane` (0 past S)
+    const float lsum = wave_sum(wj * lj);
+    float o0 = 0.f, o1 = 0.f;
+    for (int j0 = w; j0 < a.S; j0 += NW * R) {
+        if (j0 != w) load_round(j0);
 #pragma unroll
-        for (int i = 0; i < CH; ++i) ok = ok && tag_ok(wo[i], tag);
-        if (!ok) {
-#pragma unroll
-            for (int i = 0; i < CH; ++i) {
-                if (!tag_ok(wo[i], tag)) {
-                    wo[i] = poll_word(part + (size_t)(c0 + i) * PART_STRIDE + 2 + t, tag);
-                    good = good && tag_ok(wo[i], tag);
+        for (int i = 0; i < R; ++i) {
+            const int j = j0 + NW * i;           // wave-uniform
+            if (j >= a.S) break;
+            float v0, v1;
+            if (j == s) {                        // wave-uniform
+                v0 = s_own[2 * dp];
+                v1 = s_own[2 * dp + 1];
+            } else {
+                uint32_t a0 = op[i].x, t0 = op[i].y, a1 = op[i].z, t1 = op[i].w;
+                for (int k = 0; k < POLL_MAX; ++k) {
+                    const bool need = !(t0 == tag && t1 == tag);
+                    if (__builtin_amdgcn_ballot_w64(need) == 0) break;
+                    __builtin_amdgcn_s_sleep(2);
+                    const u32x4 re = ld128_dev(rp, (uint32_t)j * PB + 16u + (uint32_t)dp * 16u);
+                    const uint32_t ra0 = re.x, rt0 = re.y, ra1 = re.z, rt1 = re.w;
+                    a0 = need ? ra0 : a0;
+                    t0 = need ? rt0 : t0;
+                    a1 = need ? ra1 : a1;
+                    t1 = need ? rt1 : t1;
                 }
+                good = good && t0 == tag && t1 == tag;
+                v0 = __builtin_bit_cast(float, a0);
+                v1 = __builtin_bit_cast(float, a1);
             }
+            const float f = __builtin_bit_cast(float,
+                __builtin_amdgcn_readlane(__builtin_bit_cast(int, wj), j));
+            o0 = __builtin_fmaf(f, v0, o0);
+            o1 = __builtin_fmaf(f, v1, o1);
         }
-#pragma unroll
-        for (int i = 0; i < CH; ++i) {
-            const float w = __builtin_bit_cast(float,
-                __builtin_amdgcn_readlane(__builtin_bit_cast(int, wj), c0 + i));
-            o = __builtin_fmaf(w, tag_val(wo[i]), o);
-        }
+    }
+    if (lane < D / 2) {
+        s_fold[w][2 * lane]     = o0;
+        s_fold[w][2 * lane + 1] = o1;
     }
     // A lost partial (never observed within the poll bound) shows as NaN.
-    good = __builtin_amdgcn_ballot_w64(!good) == 0;
-    a.out[(size_t)h * D + t] = good ? f2h_rne(o / lsum) : (uint16_t)0x7E00u;
+    if (__builtin_amdgcn_ballot_w64(!good) != 0 && lane == 0) s_bad = 1;
+    __syncthreads();
+    if (t < D) {
+        float o = 0.f;
+#pragma unroll
+        for (int v = 0; v < NW; ++v) o += s_fold[v][t];
+        a.out[(size_t)h * D + t] = s_bad ? (uint16_t)0x7E00u : f2h_rne(o / lsum);
+    }
     if (t == 0) {                            // every arrival is in: reset for the slot's next call
         store_dev(ticket, 0u);
         store_dev(ticket + 1, epoch + 1u);
@@ -660,7 +710,7 @@ __global__ __launch_bounds__(WAVES * 64) void decode_tiled(DecodeArgs a) {
 #pragma unroll
         for (int r = 0; r < WAVES * 4; ++r) ls = __builtin_fmaf(f[r / 4], s_l[r], ls);
     }
-    finish_partial<D, 16, WAVES * 64>(a, h, s, M, ls, acc, epoch);
+    finish_partial<D, WAVES * 64>(a, h, s, M, ls, acc, epoch);
 }
 
 // ------------------------------------------------------- naive (w1) kernel --
@@ -755,7 +805,7 @@ __global__ __launch_bounds__(256) void decode_w1(DecodeArgs a) {
             ls  = __builtin_fmaf(f, s_l[w], ls);
         }
     }
-    finish_partial<D, 8, WAVES * 64>(a, h, s, M, ls, acc, epoch);
+    finish_partial<D, WAVES * 64>(a, h, s, M, ls, acc, epoch);
 }
 
 // ---------------------------------------------------------------- dispatch --
