@@ -35,7 +35,7 @@
 extern "C" {
 #endif
 
-#define VA_ABI_VERSION 1
+#define VA_ABI_VERSION 2
 
 /* Status codes. */
 enum {
@@ -135,6 +135,82 @@ int va_fill_normal(float* x, size_t n, uint64_t seed, void* stream);
  * `bytes`-sized device buffer, taking the best of several launch shapes
  * (probe_ceiling + read_kernel, src/voltattn.cu:64-78, 935-957). */
 int va_probe_read(size_t bytes, int reps, double* best_gbps);
+
+/* ---- grouped-query attention, batches and paged caches ----
+ * No counterpart in the reference, which decodes one sequence with one query
+ * head per K/V head from a contiguous cache (its README.md:205-206 lists GQA
+ * and paged KV as missing). The row formats, quantizer and arithmetic are the
+ * reference path's; only the tiled formats (f16+, q8+, q4+, q3+) run here,
+ * the naive ones return VA_EINVAL. Query head i of a sequence attends KV head
+ * i / (Hq / Hkv) (consecutive query heads share a KV head). */
+
+/* One sequence, Hq query heads over Hkv KV heads (Hq % Hkv == 0): b->q and
+ * b->out are [Hq][D]; k, v, sk, sv are the contiguous [Hkv][L][...] layouts of
+ * va_decode; ws holds va_ws_bytes(Hq, D, S). Each K/V row is unpacked once for
+ * all query heads that share it. Hq == Hkv is exactly va_decode. S = 0 picks
+ * the split count (va_pick_splits_gqa). */
+int va_decode_gqa(va_fmt fmt, const va_bufs* b, int Hq, int Hkv, int L, int D, int G, int S,
+                  void* stream);
+int va_pick_splits_gqa(va_fmt fmt, int Hq, int Hkv, int L, int D, int* S);
+
+/* Shape of a batch decoded from a page pool. Page p of the pool holds
+ * [Hkv][page_rows][row] payload bytes (row as for va_decode) and
+ * [Hkv][page_rows][D/G] fp16 scales; position j of sequence b is row
+ * j % page_rows of page block_table[b][j / page_rows]. A contiguous cache
+ * [Hkv][Lcap][row] per sequence is the case page_rows = Lcap (a power of two)
+ * with block_table[b] = {b}. */
+typedef struct {
+    int B;             /* sequences in the batch */
+    int Hq, Hkv;       /* query and KV heads per sequence, Hq % Hkv == 0 */
+    int D, G;          /* D in {64,128}; G in {32,64} (ignored for f16 formats) */
+    int page_rows;     /* positions per page: a power of two >= 64 */
+    int max_pages;     /* block-table row length (pages per sequence at most) */
+    int num_pages;     /* pages in the pool; ids outside [0, num_pages) are rejected */
+    int max_seq_len;   /* >= every seq_lens[b]: sizes the splits */
+} va_paged_shape;
+
+/* Device buffers of a paged batch. Alignment as va_bufs (k, v 16 bytes, 4 for
+ * q3; sk, sv 4 bytes; q 16 bytes); block_table and seq_lens 4 bytes. */
+typedef struct {
+    const void*     k;             /* K page pool */
+    const void*     v;             /* V page pool */
+    const uint16_t* sk;            /* K scale pool (quantized formats) */
+    const uint16_t* sv;            /* V scale pool */
+    const int32_t*  block_table;   /* [B][max_pages] page ids */
+    const int32_t*  seq_lens;      /* [B] positions per sequence (0 .. max_seq_len) */
+    const uint16_t* q;             /* [B][Hq][D] fp16 */
+    uint16_t*       out;           /* [B][Hq][D] fp16 */
+    float*          ws;            /* va_ws_bytes(B * Hq, D, S) bytes */
+} va_paged_bufs;
+
+/* One decode step of every sequence of the batch: per (sequence, query head)
+ * softmax(q.K^T / sqrt(D)) V over that sequence's seq_lens[b] positions.
+ * Splits are S ranges of ceil(max_seq_len / S) positions (rounded up to the
+ * kernel tile); a sequence shorter than max_seq_len leaves its later splits
+ * empty. A sequence of length 0 gives a zero output; a length above
+ * max_seq_len, or a page id outside the pool on one of its positions, gives
+ * NaN for that sequence's heads. S = 0 picks the split count
+ * (va_pick_splits_paged). Asynchronous on `stream`. */
+int va_decode_paged(va_fmt fmt, const va_paged_bufs* b, const va_paged_shape* shape, int S,
+                    void* stream);
+int va_pick_splits_paged(va_fmt fmt, const va_paged_shape* shape, int* S);
+
+/* Payload bytes and scale bytes of one page (0 for invalid arguments). */
+size_t va_page_bytes(va_fmt fmt, int Hkv, int page_rows, int D);
+size_t va_page_scale_bytes(va_fmt fmt, int Hkv, int page_rows, int D, int G);
+
+/* The cache write path: quantize-and-append n new rows per (sequence, KV
+ * head). x is fp16 [B][Hkv][n][D] (16-byte aligned); row r of sequence b is
+ * written at position start[b] + r of the page pool `pages` (+ `scales`,
+ * quantized formats), laid out as in va_paged_shape (page_rows may be any
+ * value >= 1 here). Quantized formats apply the reference's quantizer
+ * (quantize(), src/voltattn.cu:705-745) to the fp16 values, bit-exact with
+ * va_quantize on the same values; f16 formats copy. Rows whose position lies
+ * past max_pages * page_rows, or on a page id outside [0, num_pages), are not
+ * written. The fields Hq and max_seq_len of `shape` are unused. */
+int va_append_kv(va_fmt fmt, const uint16_t* x, int n, const int32_t* start,
+                 const int32_t* block_table, const va_paged_shape* shape, void* pages,
+                 uint16_t* scales, void* stream);
 
 /* ---- runtime shims (the reference calls the CUDA runtime directly:
  *      cudaMalloc/cudaMemcpy/cudaFree/cudaEvent*, src/voltattn.cu:863-895, 936-955,

@@ -1,0 +1,90 @@
+"""Pins of the CPU oracle's grouped-query and paged forms (oracle/batch.py).
+
+The per-head arithmetic is the reference's reference() (src/voltattn.cu:769-794,
+pinned in test_oracle_reference.py); these tests pin what is layered on it:
+the query-head -> KV-head mapping (closed forms that a wrong mapping fails, and
+an independent float64 brute force) and the page-table addressing (a
+hand-laid table and a scatter/gather round trip)."""
+import numpy as np
+import pytest
+
+import oracle
+from oracle import batch
+
+
+def _f16(x):
+    return np.asarray(x, np.float32).astype(np.float16).view(np.uint16)
+
+
+def _brute(kd, vd, q16, Hq, Hkv, L, D):
+    """Textbook softmax attention in float64 with query head h on KV head h // (Hq/Hkv)."""
+    k = kd.reshape(Hkv, L, D).astype(np.float64)
+    v = vd.reshape(Hkv, L, D).astype(np.float64)
+    q = q16.view(np.float16).astype(np.float64).reshape(Hq, D)
+    out = np.empty((Hq, D))
+    g = Hq // Hkv
+    for h in range(Hq):
+        s = k[h // g] @ q[h] / np.sqrt(D)
+        p = np.exp(s - s.max())
+        out[h] = (p / p.sum()) @ v[h // g]
+    return out.ravel()
+
+
+def test_gqa_equal_heads_is_the_reference():
+    rng = np.random.default_rng(1)
+    H, L, D = 3, 40, 64
+    kd = rng.standard_normal(H * L * D).astype(np.float32)
+    vd = rng.standard_normal(H * L * D).astype(np.float32)
+    q = _f16(rng.standard_normal(H * D))
+    np.testing.assert_array_equal(batch.reference_gqa(kd, vd, q, H, H, L, D),
+                                  oracle.reference(kd, vd, q, H, L, D))
+
+
+def test_gqa_mapping_closed_form():
+    # V of KV head j is the constant j+1, so every output of query head h equals
+    # (h // (Hq/Hkv)) + 1 whatever K and q are; h % Hkv (a plausible slip) fails.
+    Hq, Hkv, L, D = 12, 3, 17, 64
+    rng = np.random.default_rng(2)
+    kd = rng.standard_normal(Hkv * L * D).astype(np.float32)
+    vd = np.repeat(np.arange(1, Hkv + 1, dtype=np.float32), L * D)
+    q = _f16(rng.standard_normal(Hq * D))
+    out = batch.reference_gqa(kd, vd, q, Hq, Hkv, L, D).reshape(Hq, D)
+    want = (np.arange(Hq) // (Hq // Hkv) + 1).astype(np.float32)
+    np.testing.assert_allclose(out, np.repeat(want[:, None], D, axis=1), rtol=1e-6)
+
+
+@pytest.mark.parametrize("Hq,Hkv,L,D", [(8, 2, 33, 64), (14, 2, 5, 128), (6, 6, 1, 64)])
+def test_gqa_matches_float64_brute_force(Hq, Hkv, L, D):
+    rng = np.random.default_rng(Hq * 100 + L)
+    kd = rng.standard_normal(Hkv * L * D).astype(np.float32)
+    vd = rng.standard_normal(Hkv * L * D).astype(np.float32)
+    q = _f16(rng.standard_normal(Hq * D))
+    got = batch.reference_gqa(kd, vd, q, Hq, Hkv, L, D)
+    np.testing.assert_allclose(got, _brute(kd, vd, q, Hq, Hkv, L, D), rtol=1e-6, atol=1e-7)
+
+
+def test_paged_addressing_hand_laid():
+    # 2 KV heads, page_rows 4, one row = 1 value equal to its (head, position) id
+    Hkv, P, L = 2, 4, 10
+    rows = np.array([[[100 * h + j] for j in range(L)] for h in range(Hkv)], np.int32)
+    table = np.array([5, 0, 3])              # positions 0-3 -> page 5, 4-7 -> 0, 8-9 -> 3
+    pool = np.full((6, Hkv, P, 1), -1, np.int32)
+    batch.scatter_rows(pool, rows, table, P)
+    assert pool[5, 1, 2, 0] == 102           # head 1, position 2
+    assert pool[0, 0, 3, 0] == 7             # head 0, position 7
+    assert pool[3, 1, 1, 0] == 109           # head 1, position 9
+    assert pool[3, 0, 2, 0] == -1            # past L: untouched
+    assert np.all(pool[[1, 2, 4]] == -1)     # pages outside the table: untouched
+    np.testing.assert_array_equal(batch.gather_rows(pool, table, L, P), rows)
+
+
+def test_paged_round_trip_random():
+    rng = np.random.default_rng(7)
+    Hkv, P, W = 3, 8, 5
+    for L in (1, 7, 8, 9, 64, 77):
+        npg = -(-L // P)
+        table = rng.permutation(npg + 4)[:npg]
+        pool = rng.integers(0, 255, (npg + 4, Hkv, P, W), dtype=np.uint8)
+        rows = rng.integers(0, 255, (Hkv, L, W), dtype=np.uint8)
+        batch.scatter_rows(pool, rows, table, P)
+        np.testing.assert_array_equal(batch.gather_rows(pool, table, L, P), rows)

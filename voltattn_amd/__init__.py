@@ -28,6 +28,8 @@ __all__ = [
     "payload_bytes", "scale_bytes", "split_chunk", "pick_splits", "quantize", "f32_to_f16",
     "fill_normal", "probe_read", "device_info", "device_count", "DeviceBuffer", "Event",
     "Stream", "Graph", "sync", "lib", "LIB_PATH", "fmt_bits", "is_f16", "check",
+    "PagedShape", "PagedBufs", "decode_gqa", "pick_splits_gqa", "decode_paged",
+    "pick_splits_paged", "page_bytes", "page_scale_bytes", "append_kv", "row_bytes",
 ]
 
 # VOLTATTN_LIB may name another build of the same library (tuning variants).
@@ -42,6 +44,16 @@ _P, _I, _SZ, _U64 = C.c_void_p, C.c_int, C.c_size_t, C.c_uint64
 
 class _Bufs(C.Structure):
     _fields_ = [("k", _P), ("v", _P), ("sk", _P), ("sv", _P), ("q", _P), ("out", _P), ("ws", _P)]
+
+
+class _PagedShape(C.Structure):
+    _fields_ = [("B", _I), ("Hq", _I), ("Hkv", _I), ("D", _I), ("G", _I), ("page_rows", _I),
+                ("max_pages", _I), ("num_pages", _I), ("max_seq_len", _I)]
+
+
+class _PagedBufs(C.Structure):
+    _fields_ = [("k", _P), ("v", _P), ("sk", _P), ("sv", _P), ("block_table", _P),
+                ("seq_lens", _P), ("q", _P), ("out", _P), ("ws", _P)]
 
 
 class _DevInfo(C.Structure):
@@ -70,6 +82,13 @@ _sig("va_quantize", _I, _I, _I, _P, _SZ, _I, _P, _P, _P)
 _sig("va_f32_to_f16", _I, _P, _SZ, _P, _P)
 _sig("va_fill_normal", _I, _P, _SZ, _U64, _P)
 _sig("va_probe_read", _I, _SZ, _I, C.POINTER(C.c_double))
+_sig("va_decode_gqa", _I, _I, C.POINTER(_Bufs), _I, _I, _I, _I, _I, _I, _P)
+_sig("va_pick_splits_gqa", _I, _I, _I, _I, _I, _I, C.POINTER(_I))
+_sig("va_decode_paged", _I, _I, C.POINTER(_PagedBufs), C.POINTER(_PagedShape), _I, _P)
+_sig("va_pick_splits_paged", _I, _I, C.POINTER(_PagedShape), C.POINTER(_I))
+_sig("va_page_bytes", _SZ, _I, _I, _I, _I)
+_sig("va_page_scale_bytes", _SZ, _I, _I, _I, _I, _I)
+_sig("va_append_kv", _I, _I, _P, _I, _P, _P, C.POINTER(_PagedShape), _P, _P, _P)
 _sig("va_device_count", _I, C.POINTER(_I))
 _sig("va_set_device", _I, _I)
 _sig("va_device_info", _I, C.POINTER(_DevInfo))
@@ -174,6 +193,92 @@ def decode_splits(f: Fmt, b: DeviceBufs, H: int, L: int, D: int, S: int, G: int 
 
 def merge(ws: int, out: int, H: int, D: int, S: int, stream=None) -> None:
     check(lib.va_merge(ws, out, H, D, S, _stream(stream)))
+
+
+def decode_gqa(f: Fmt, b: DeviceBufs, Hq: int, Hkv: int, L: int, D: int, S: int = 0, G: int = 64,
+               stream=None) -> None:
+    """One sequence, Hq query heads over Hkv KV heads (query head h reads KV head
+    h // (Hq // Hkv)); q/out are [Hq][D], K/V [Hkv][L][row]. S = 0 picks it."""
+    cb = b._c()
+    check(lib.va_decode_gqa(int(f), C.byref(cb), Hq, Hkv, L, D, G, S, _stream(stream)))
+
+
+def pick_splits_gqa(f: Fmt, Hq: int, Hkv: int, L: int, D: int) -> int:
+    s = _I(0)
+    check(lib.va_pick_splits_gqa(int(f), Hq, Hkv, L, D, C.byref(s)))
+    return s.value
+
+
+@dataclass
+class PagedShape:
+    """va_paged_shape: a batch of B sequences over a page pool of num_pages pages,
+    each holding [Hkv][page_rows][row] (+ [Hkv][page_rows][D/G] fp16 scales)."""
+    B: int
+    Hq: int
+    Hkv: int
+    D: int
+    G: int
+    page_rows: int
+    max_pages: int
+    num_pages: int
+    max_seq_len: int
+
+    def _c(self) -> _PagedShape:
+        return _PagedShape(self.B, self.Hq, self.Hkv, self.D, self.G, self.page_rows,
+                           self.max_pages, self.num_pages, self.max_seq_len)
+
+
+@dataclass
+class PagedBufs:
+    """va_paged_bufs: device pointers as ints (0 = NULL)."""
+    K: int = 0
+    V: int = 0
+    scK: int = 0
+    scV: int = 0
+    block_table: int = 0
+    seq_lens: int = 0
+    q: int = 0
+    out: int = 0
+    ws: int = 0
+
+    def _c(self) -> _PagedBufs:
+        return _PagedBufs(self.K or None, self.V or None, self.scK or None, self.scV or None,
+                          self.block_table or None, self.seq_lens or None, self.q or None,
+                          self.out or None, self.ws or None)
+
+
+def decode_paged(f: Fmt, b: PagedBufs, shape: PagedShape, S: int = 0, stream=None) -> None:
+    """One decode step of every sequence of a paged batch (q/out [B][Hq][D])."""
+    cb, cs = b._c(), shape._c()
+    check(lib.va_decode_paged(int(f), C.byref(cb), C.byref(cs), S, _stream(stream)))
+
+
+def pick_splits_paged(f: Fmt, shape: PagedShape) -> int:
+    s = _I(0)
+    cs = shape._c()
+    check(lib.va_pick_splits_paged(int(f), C.byref(cs), C.byref(s)))
+    return s.value
+
+
+def page_bytes(f: Fmt, Hkv: int, page_rows: int, D: int) -> int:
+    return lib.va_page_bytes(int(f), Hkv, page_rows, D)
+
+
+def page_scale_bytes(f: Fmt, Hkv: int, page_rows: int, D: int, G: int) -> int:
+    return lib.va_page_scale_bytes(int(f), Hkv, page_rows, D, G)
+
+
+def append_kv(f: Fmt, x: int, n: int, start: int, block_table: int, shape: PagedShape, pages: int,
+              scales: int = 0, stream=None) -> None:
+    """Quantize-and-append n new fp16 rows per (sequence, KV head), x [B][Hkv][n][D],
+    at positions start[b] + r of a paged cache."""
+    cs = shape._c()
+    check(lib.va_append_kv(int(f), x, n, start, block_table, C.byref(cs), pages, scales or None,
+                           _stream(stream)))
+
+
+def row_bytes(f: Fmt, D: int) -> int:
+    return D * fmt_bits(f) // 8
 
 
 def ws_bytes(H: int, D: int, S: int) -> int:

@@ -1,0 +1,287 @@
+// va_codec.hpp — lane layouts and lane codecs of the tiled decode kernels.
+//
+// Layout: a position row of ROWB compressed bytes is read by LP lanes, each
+// taking LB = 16 contiguous bytes (12 for q3) with one buffer load, so one
+// wave-wide load covers PPW = 64/LP consecutive rows (1 KiB; 768 B for q3).
+//
+// Codecs: a lane owns EPL consecutive elements of a row. `unpack` turns the
+// lane's stored codes into NP exact fp16 pairs with bit operations only (no
+// per-element convert), once per row; `dot` and `axpy` then consume the pairs
+// for every query head that shares the row (grouped-query attention reuses
+// one unpack for several heads):
+//   * K: v_dot2_f32_f16 against the unscaled fp16 q (f16, q8, q4: products of
+//     two fp16 values are exact in fp32), or v_fma_mix_f32 against fp32 q (q3);
+//   * V: v_fma_mix_f32, o_e += ev * code_e with an fp16 operand and fp32
+//     accumulation (P.V stays fp32).
+// The fp16 "magic" construction: OR-ing a code n (< 2^10 / 2^r) shifted left by
+// r into the mantissa of 1024.0 (0x6400) gives 1024 + 2^r n exactly; one packed
+// fp16 subtract of 1024 + 2^r * offset then leaves 2^r * v. The magic constant
+// lives in a VGPR (`magic()`, made once per kernel) so mask-and-insert is one
+// v_and_or_b32 (a gfx9 VOP3 reads one scalar constant; mask and magic cannot
+// both be literals).
+//
+// Interface: QReg (one query head's slice in codec form), load_q(QReg&, q
+// slice, qs) with qs = log2(e)/sqrt(D), magic(), unpack(w, magic, p[NP]),
+// dot(p, QReg) -> q.k in log2 units, axpy(p, ev, o), finish(o) (per-element
+// fix-up once at the end).
+#pragma once
+#include "va_device.hpp"
+
+#include <utility>
+
+namespace va {
+
+template <int KIND, int D> struct Tile {
+    static constexpr int ROWB = RowBytes<KIND, D>::value;   // bytes per row
+    static constexpr int LB   = KIND == KQ3 ? 12 : 16;      // bytes per lane per row
+    static constexpr int LP   = ROWB / LB;                  // lanes per row
+    static constexpr int PPW  = 64 / LP;                    // rows per wave load
+    static constexpr int EPL  = D / LP;                     // elements per lane
+    static_assert(ROWB % LB == 0 && 64 % LP == 0 && LP <= 16, "lane split");
+};
+
+// Rows per lane per tile and tensor (U). Each kind is instantiated for two
+// depths; the dispatch picks one per kind.
+template <int KIND> struct UnrollSet;
+template <> struct UnrollSet<KF16> { static constexpr int a = 4, b = 8; };
+template <> struct UnrollSet<KQ8>  { static constexpr int a = 2, b = 4; };
+template <> struct UnrollSet<KQ4>  { static constexpr int a = 2, b = 4; };
+template <> struct UnrollSet<KQ3>  { static constexpr int a = 2, b = 4; };
+
+template <int KIND> struct LaneLoad { using type = u32x4; };
+template <> struct LaneLoad<KQ3> { using type = u32x3; };
+
+template <int KIND>
+__device__ __forceinline__ typename LaneLoad<KIND>::type
+lane_load(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+    if constexpr (KIND == KQ3) return ld96(r, voff, soff);
+    else return ld128(r, voff, soff);
+}
+
+typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ h2 as_h2(uint32_t x) { return __builtin_bit_cast(h2, x); }
+__device__ __forceinline__ h2 hh(float a, float b) { return h2{(_Float16)a, (_Float16)b}; }
+
+#define VA_VGPR_CONST(dst, imm) asm volatile("v_mov_b32 %0, " #imm : "=v"(dst))
+
+// Load a lane's q slice (EPL fp16 values, 16-byte aligned) as raw dwords.
+template <int EPL>
+__device__ __forceinline__ void load_q_words(uint32_t (&qw)[EPL / 2], const uint16_t* qh) {
+#pragma unroll
+    for (int c = 0; c < EPL / 8; ++c) {
+        const u32x4 w = reinterpret_cast<const u32x4*>(qh)[c];
+        qw[4 * c] = w.x; qw[4 * c + 1] = w.y; qw[4 * c + 2] = w.z; qw[4 * c + 3] = w.w;
+    }
+}
+
+template <int KIND> struct Codec;
+
+// Pairs (2k, 2k+1) as consecutive elements: the f16 and q8 layouts.
+template <int NP>
+__device__ __forceinline__ float dot_pairs(const h2 (&p)[NP], const h2 (&q)[NP]) {
+    float a = 0.f;
+#pragma unroll
+    for (int k = 0; k < NP; ++k) a = __builtin_amdgcn_fdot2(p[k], q[k], a, false);
+    return a;
+}
+template <int NP>
+__device__ __forceinline__ void axpy_pairs(const h2 (&p)[NP], float ev, float* o) {
+#pragma unroll
+    for (int k = 0; k < NP; ++k) {
+        o[2 * k]     = __builtin_fmaf(ev, (float)p[k].x, o[2 * k]);
+        o[2 * k + 1] = __builtin_fmaf(ev, (float)p[k].y, o[2 * k + 1]);
+    }
+}
+
+// f16: 8 halves per lane, element 2k+j in half j of dword k.
+template <> struct Codec<KF16> {
+    static constexpr int EPL = 8, NP = 4;
+    struct QReg { h2 q[NP]; float qs; };
+    __device__ static void load_q(QReg& r, const uint16_t* qh, float qs) {
+        uint32_t qw[4];
+        load_q_words<8>(qw, qh);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) r.q[i] = as_h2(qw[i]);
+        r.qs = qs;
+    }
+    __device__ static uint32_t magic() { return 0u; }
+    __device__ static void unpack(const u32x4& w, uint32_t, h2 (&p)[NP]) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) p[i] = as_h2(w[i]);
+    }
+    __device__ static float dot(const h2 (&p)[NP], const QReg& r) { return dot_pairs<NP>(p, r.q) * r.qs; }
+    __device__ static void axpy(const h2 (&p)[NP], float ev, float* o) { axpy_pairs<NP>(p, ev, o); }
+    __device__ static void finish(float*) {}
+};
+
+// q8: 16 int8 per lane, element 4i+b in byte b of dword i. xor 0x80 makes the
+// bytes u = v + 128; v_perm_b32 places bytes (b0, b1) / (b2, b3) under the
+// 0x64 magic byte: fp16 pair (1024 + u, 1024 + u'), minus 1152 -> (v, v').
+// Pair k holds elements (2k, 2k+1).
+template <> struct Codec<KQ8> {
+    static constexpr int EPL = 16, NP = 8;
+    struct QReg { h2 q[NP]; float qs; };
+    __device__ static void load_q(QReg& r, const uint16_t* qh, float qs) {
+        uint32_t qw[8];
+        load_q_words<16>(qw, qh);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) r.q[i] = as_h2(qw[i]);
+        r.qs = qs;
+    }
+    __device__ static uint32_t magic() { uint32_t m; VA_VGPR_CONST(m, 0x64646464); return m; }
+    __device__ static void unpack(const u32x4& w, uint32_t magic, h2 (&p)[NP]) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const uint32_t u = w[i] ^ 0x80808080u;
+            p[2 * i]     = as_h2(__builtin_amdgcn_perm(magic, u, 0x04010400u)) - hh(1152.f, 1152.f);
+            p[2 * i + 1] = as_h2(__builtin_amdgcn_perm(magic, u, 0x04030402u)) - hh(1152.f, 1152.f);
+        }
+    }
+    __device__ static float dot(const h2 (&p)[NP], const QReg& r) { return dot_pairs<NP>(p, r.q) * r.qs; }
+    __device__ static void axpy(const h2 (&p)[NP], float ev, float* o) { axpy_pairs<NP>(p, ev, o); }
+    __device__ static void finish(float*) {}
+};
+
+// q4: 32 nibbles per lane; element 8i+j sits in nibble j of dword i. Masking
+// nibbles (0, 4) / (1, 5) in place and (2, 6) / (3, 7) after a shift by 8 under
+// the 1024.0 magic gives the exact pairs
+//   P0 = (e0, e4) = v,  P1 = (e1, e5) = 16v,  P2 = (e2, e6) = v,  P3 = (e3, e7) = 16v;
+// the 16v pairs accumulate separately (scaled by 1/16 once) for K and use
+// ev/16 for V. Pair 4i+c is Pc of dword i.
+template <> struct Codec<KQ4> {
+    static constexpr int EPL = 32, NP = 16;
+    struct QReg { h2 q[NP]; float qs; };     // q[4i+c] pairs the elements of P_c of dword i
+    __device__ static void load_q(QReg& r, const uint16_t* qh, float qs) {
+        uint32_t qw[16];
+        load_q_words<32>(qw, qh);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            // halves of elements 8i..8i+7: qw[4i] = (e0, e1), +1 = (e2, e3), +2 = (e4, e5), +3 = (e6, e7)
+            r.q[4 * i + 0] = as_h2(__builtin_amdgcn_perm(qw[4 * i + 2], qw[4 * i], 0x05040100u));      // (e0, e4)
+            r.q[4 * i + 1] = as_h2(__builtin_amdgcn_perm(qw[4 * i + 2], qw[4 * i], 0x07060302u));      // (e1, e5)
+            r.q[4 * i + 2] = as_h2(__builtin_amdgcn_perm(qw[4 * i + 3], qw[4 * i + 1], 0x05040100u));  // (e2, e6)
+            r.q[4 * i + 3] = as_h2(__builtin_amdgcn_perm(qw[4 * i + 3], qw[4 * i + 1], 0x07060302u));  // (e3, e7)
+        }
+        r.qs = qs;
+    }
+    __device__ static uint32_t magic() { uint32_t m; VA_VGPR_CONST(m, 0x64006400); return m; }
+    __device__ static void unpack(const u32x4& w, uint32_t magic, h2 (&p)[NP]) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const uint32_t x = w[i], x8 = w[i] >> 8;
+            p[4 * i + 0] = as_h2((x & 0x000F000Fu) | magic) - hh(1032.f, 1032.f);
+            p[4 * i + 1] = as_h2((x & 0x00F000F0u) | magic) - hh(1152.f, 1152.f);
+            p[4 * i + 2] = as_h2((x8 & 0x000F000Fu) | magic) - hh(1032.f, 1032.f);
+            p[4 * i + 3] = as_h2((x8 & 0x00F000F0u) | magic) - hh(1152.f, 1152.f);
+        }
+    }
+    __device__ static float dot(const h2 (&p)[NP], const QReg& r) {
+        float a1 = 0.f, a16 = 0.f;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            a1  = __builtin_amdgcn_fdot2(p[4 * i + 0], r.q[4 * i + 0], a1, false);
+            a16 = __builtin_amdgcn_fdot2(p[4 * i + 1], r.q[4 * i + 1], a16, false);
+            a1  = __builtin_amdgcn_fdot2(p[4 * i + 2], r.q[4 * i + 2], a1, false);
+            a16 = __builtin_amdgcn_fdot2(p[4 * i + 3], r.q[4 * i + 3], a16, false);
+        }
+        return __builtin_fmaf(a16, 0.0625f, a1) * r.qs;
+    }
+    __device__ static void axpy(const h2 (&p)[NP], float ev, float* o) {
+        const float ev16 = ev * 0.0625f;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            o[8 * i + 0] = __builtin_fmaf(ev,   (float)p[4 * i + 0].x, o[8 * i + 0]);
+            o[8 * i + 4] = __builtin_fmaf(ev,   (float)p[4 * i + 0].y, o[8 * i + 4]);
+            o[8 * i + 1] = __builtin_fmaf(ev16, (float)p[4 * i + 1].x, o[8 * i + 1]);
+            o[8 * i + 5] = __builtin_fmaf(ev16, (float)p[4 * i + 1].y, o[8 * i + 5]);
+            o[8 * i + 2] = __builtin_fmaf(ev,   (float)p[4 * i + 2].x, o[8 * i + 2]);
+            o[8 * i + 6] = __builtin_fmaf(ev,   (float)p[4 * i + 2].y, o[8 * i + 6]);
+            o[8 * i + 3] = __builtin_fmaf(ev16, (float)p[4 * i + 3].x, o[8 * i + 3]);
+            o[8 * i + 7] = __builtin_fmaf(ev16, (float)p[4 * i + 3].y, o[8 * i + 7]);
+        }
+    }
+    __device__ static void finish(float*) {}
+};
+
+// q3: 32 3-bit fields per lane, element e at bits [3e, 3e+3) of the lane's
+// 96-bit little-endian word (v + 4). Eight 32-bit windows of that word (one
+// alignbit/shift each) hold two pairs apiece: a field at bit r of the low half
+// and one at bit 16 + r' of the high half, r, r' <= 7. The 16 pairs:
+//   window s = 0, 6, 12, 36, 42, 48: (a, a+6) at (0, 18) and (a+1, a+7) at (3, 21), a = s/3
+//   window s = 68, 74:               (a, a+4) at (4, 16) and (a+1, a+5) at (7, 19), a = (s+4)/3
+// A pair becomes (2^r v, 2^r' v') exactly; K uses fp32 q pre-scaled by 2^-r,
+// V accumulates 2^r v and finish() scales o_e by 2^-r once.
+struct Q3Pair { int a, b, s, r, rp; };
+__device__ constexpr Q3Pair kQ3Pairs[16] = {
+    {0, 6, 0, 0, 2},    {1, 7, 0, 3, 5},    {2, 8, 6, 0, 2},    {3, 9, 6, 3, 5},
+    {4, 10, 12, 0, 2},  {5, 11, 12, 3, 5},  {12, 18, 36, 0, 2}, {13, 19, 36, 3, 5},
+    {14, 20, 42, 0, 2}, {15, 21, 42, 3, 5}, {16, 22, 48, 0, 2}, {17, 23, 48, 3, 5},
+    {24, 28, 68, 4, 0}, {25, 29, 68, 7, 3}, {26, 30, 74, 4, 0}, {27, 31, 74, 7, 3},
+};
+__device__ constexpr int q3_shift(int e) {          // r of element e in its pair
+    for (int i = 0; i < 16; ++i) {
+        if (kQ3Pairs[i].a == e) return kQ3Pairs[i].r;
+        if (kQ3Pairs[i].b == e) return kQ3Pairs[i].rp;
+    }
+    return 0;
+}
+
+template <> struct Codec<KQ3> {
+    static constexpr int EPL = 32, NP = 16;
+    struct QReg { float q[32]; };
+    __device__ static uint32_t window(const u32x3& w, int s) {
+        if (s == 0) return w.x;
+        if (s < 32) return __builtin_amdgcn_alignbit(w.y, w.x, s);
+        if (s == 32) return w.y;
+        if (s < 64) return __builtin_amdgcn_alignbit(w.z, w.y, s - 32);
+        return w.z >> (s - 64);
+    }
+    template <int I>
+    __device__ static h2 pair(const u32x3& w, uint32_t magic) {
+        constexpr Q3Pair P = kQ3Pairs[I];
+        constexpr uint32_t mask = (7u << P.r) | (7u << (16 + P.rp));
+        return as_h2((window(w, P.s) & mask) | magic) -
+               hh(1024.f + 4.f * (float)(1 << P.r), 1024.f + 4.f * (float)(1 << P.rp));
+    }
+    __device__ static void load_q(QReg& r, const uint16_t* qh, float qs) {
+        uint32_t qw[16];
+        load_q_words<32>(qw, qh);
+#pragma unroll
+        for (int e = 0; e < 32; ++e) {
+            const float x = (e & 1) ? h2f_hi(qw[e / 2]) : h2f_lo(qw[e / 2]);
+            r.q[e] = x * qs * (1.0f / (float)(1 << q3_shift(e)));
+        }
+    }
+    __device__ static uint32_t magic() { uint32_t m; VA_VGPR_CONST(m, 0x64006400); return m; }
+    template <int... I>
+    __device__ static void unpack_all(const u32x3& w, uint32_t magic, h2 (&p)[NP],
+                                      std::integer_sequence<int, I...>) {
+        ((p[I] = pair<I>(w, magic)), ...);
+    }
+    __device__ static void unpack(const u32x3& w, uint32_t magic, h2 (&p)[NP]) {
+        unpack_all(w, magic, p, std::make_integer_sequence<int, NP>{});
+    }
+    __device__ static float dot(const h2 (&p)[NP], const QReg& r) {
+        float a0 = 0.f, a1 = 0.f;
+#pragma unroll
+        for (int i = 0; i < NP; ++i) {
+            float& a = (i & 1) ? a1 : a0;
+            a = __builtin_fmaf((float)p[i].x, r.q[kQ3Pairs[i].a], a);
+            a = __builtin_fmaf((float)p[i].y, r.q[kQ3Pairs[i].b], a);
+        }
+        return a0 + a1;
+    }
+    __device__ static void axpy(const h2 (&p)[NP], float ev, float* o) {
+#pragma unroll
+        for (int i = 0; i < NP; ++i) {
+            o[kQ3Pairs[i].a] = __builtin_fmaf(ev, (float)p[i].x, o[kQ3Pairs[i].a]);
+            o[kQ3Pairs[i].b] = __builtin_fmaf(ev, (float)p[i].y, o[kQ3Pairs[i].b]);
+        }
+    }
+    __device__ static void finish(float* o) {
+#pragma unroll
+        for (int e = 0; e < 32; ++e) o[e] *= 1.0f / (float)(1 << q3_shift(e));
+    }
+};
+
+} // namespace va

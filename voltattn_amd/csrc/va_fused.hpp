@@ -1,0 +1,235 @@
+// va_fused.hpp — end of a split-L work-group: the partial (m, l, o[D]) of each
+// of its query heads, and the fused second pass (the last work-group of a
+// merge group merges all of its partials, so one decode step is one kernel).
+//
+// The ticket lines and the partial store are file-static device arrays, so
+// every translation unit that includes this header (one code object each)
+// owns its own set; calls rotate over TICKET_SLOTS slots of them.
+#pragma once
+#include "va_device.hpp"
+#include "va_kernels.hpp"
+
+namespace va {
+
+// Ticket lines and partial store of the fused merge (zero-initialised with
+// the code object; layout in va_kernels.hpp).
+static __device__ __align__(256) unsigned g_tickets[TICKET_SLOTS * TICKET_MAXH * TICKET_STRIDE];
+static __device__ __align__(256) uint64_t g_parts[(size_t)TICKET_SLOTS * PART_CAP * PART_STRIDE];
+
+constexpr int POLL_MAX = 1 << 12;   // bound on re-reads of one in-flight word
+
+__device__ __forceinline__ uint64_t tagged(float v, uint32_t tag) {
+    return ((uint64_t)tag << 32) | __builtin_bit_cast(uint32_t, v);
+}
+
+// 16 bytes (two tagged words) from the device coherence point (sc1, as the
+// relaxed agent-scope loads of va_device.hpp). The compiler tracks these like
+// any buffer load, so a round of them is in flight at once.
+__device__ __forceinline__ u32x4 ld128_dev(__amdgpu_buffer_rsrc_t r, uint32_t voff) {
+    return __builtin_amdgcn_raw_buffer_load_b128(r, voff, 0, 16 /* sc1 */);
+}
+
+// The call epoch of merge group mg on this call's ticket slot; read at kernel
+// start (the merge of this call advances it only after every group arrived).
+__device__ __forceinline__ unsigned read_epoch(const DecodeArgs& a, int mg) {
+    if (a.ticket_slot < 0) return 0u;
+    return load_dev(g_tickets + ((size_t)a.ticket_slot * TICKET_MAXH + mg) * TICKET_STRIDE + 1);
+}
+
+// Where a work-group's partials go. A merge group is the set of S splits of
+// one (sequence, KV head, query sub-group); it owns QG query slots, of which
+// the first nq are real query heads, with global (batch-flattened) indexes
+// oh0, oh0 + 1, ...
+struct Route {
+    int mg;    // merge group = blockIdx.x / S
+    int s;     // split
+    int nq;    // valid query slots
+    int oh0;   // global index of query slot 0: rows of q, out and ws
+};
+
+// Work-group of NT threads; thread t < D holds acc[q] = o[t] of query slot q's
+// partial, and M[q], ls[q] (slots >= nq are ignored).
+//
+// Two-pass form (ticket_slot < 0): the partials go to ws[(oh0+q)*S + s].
+//
+// Fused form: every value of a partial is stored as one 64-bit word
+// (tag << 32 | fp32 bits), tag = (epoch << 11 | mg << 1 | 1), unique per merge
+// group and call and never zero; a partial is PART_STRIDE words: m, l,
+// o[0..D), and partial (q, s) of merge group mg sits at (mg*QG + q)*S + s.
+// Thread NT-1 (which stores nothing, so its wait covers only its own atomic)
+// takes the group's ticket without waiting for the stores to complete; the
+// work-group that completes the ticket merges. It keeps its own partials in
+// LDS and reads the others with 16-byte coherent loads, each carrying two
+// words; a word whose tag is stale belongs to a group that has already arrived
+// and issued its stores, so it is re-read (bounded) until it lands.
+//
+// The merge spreads the loads over all NT/64 waves (coherent loads are
+// serviced one instruction at a time): per query slot, lane j of every wave
+// reads split j's (m, l); wave w folds splits j = w, w + NW, ... in increasing
+// order into lane-pair columns (2i, 2i+1) with split j's weight read by
+// readlane; the NW wave sums are added in wave order through LDS. The order is
+// fixed, so the result does not depend on arrival order. A merged l of zero
+// (no positions) gives a zero output; a non-finite one (an invalid input that
+// the kernel flagged with l = NaN) gives NaN. Needs S <= 64.
+template <int D, int NT, int QG>
+__device__ void finish_partial(const DecodeArgs& a, const Route& rt, const float (&M)[QG],
+                               const float (&ls)[QG], const float (&acc)[QG], unsigned epoch) {
+    constexpr int NW = NT / 64;
+    constexpr int R  = 4;                       // o-pair loads per wave per round
+    constexpr uint32_t PB = PART_STRIDE * 8;    // bytes per partial (16-byte multiple)
+    static_assert(PB % 16 == 0 && D + 2 <= PART_STRIDE, "partial layout");
+    const int t = (int)threadIdx.x;
+    const int S = a.S, s = rt.s;
+    if (a.ticket_slot < 0) {
+        if (t < D) {
+#pragma unroll
+            for (int q = 0; q < QG; ++q) {
+                if (q >= rt.nq) break;
+                float* slot = a.ws + ((size_t)(rt.oh0 + q) * S + s) * (D + 2);
+                store_dev(slot + 2 + t, acc[q]);
+                if (t == 0) {
+                    store_dev(slot, M[q]);
+                    store_dev(slot + 1, ls[q]);
+                }
+            }
+        }
+        return;
+    }
+    __shared__ int   s_last, s_bad;
+    __shared__ float s_own[QG][D + 2];          // o[0..D), m, l of this group's partials
+    __shared__ float s_fold[QG][NW][D];
+    unsigned* ticket = g_tickets + ((size_t)a.ticket_slot * TICKET_MAXH + rt.mg) * TICKET_STRIDE;
+    if (t == NT - 1)
+        s_last = __hip_atomic_fetch_add(ticket, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+                 (unsigned)(S - 1);
+    const uint32_t tag = (epoch << 11) | ((uint32_t)rt.mg << 1) | 1u;
+    uint64_t* base = g_parts + ((size_t)a.ticket_slot * PART_CAP + (size_t)rt.mg * QG * S) * PART_STRIDE;
+    if (t < D) {
+#pragma unroll
+        for (int q = 0; q < QG; ++q) {
+            if (q >= rt.nq) break;
+            uint64_t* mine = base + ((size_t)q * S + s) * PART_STRIDE;
+            store_dev(mine + 2 + t, tagged(acc[q], tag));
+            s_own[q][t] = acc[q];
+            if (t == 0) {
+                store_dev(mine, tagged(M[q], tag));
+                store_dev(mine + 1, tagged(ls[q], tag));
+                s_own[q][D] = M[q];
+                s_own[q][D + 1] = ls[q];
+            }
+        }
+        if (t == 0) s_bad = 0;
+    }
+    __syncthreads();
+    if (!s_last) return;
+
+    const int w    = uniform(t >> 6);
+    const int lane = t & 63;
+    const int dp   = min(lane, D / 2 - 1);     // o pair of this lane: dims 2dp, 2dp + 1
+    const int jl   = min(lane, S - 1);
+    const bool in_s = lane < S, own = lane == s;
+    bool good = true;
+    float lsum[QG];
+#pragma unroll
+    for (int q = 0; q < QG; ++q) {
+        lsum[q] = 1.f;
+        if (q >= rt.nq) break;
+        const __amdgpu_buffer_rsrc_t rp = make_rsrc(base + (size_t)q * S * PART_STRIDE, (uint32_t)S * PB);
+        // (m, l) of split `lane` (words 0, 1 of its partial), and the first
+        // round of this wave's o pairs, issued together. The words are taken
+        // out of each 16-byte vector right after its load (carrying the vector
+        // through the re-read loop was mis-compiled).
+        const u32x4 ml = ld128_dev(rp, (uint32_t)jl * PB);
+        uint32_t op[R][4];
+        auto load_round = [&](int j0) {
+#pragma unroll
+            for (int i = 0; i < R; ++i) {
+                const int j = j0 + NW * i;       // wave-uniform: no load past the last split
+                if (j < S) {
+                    const u32x4 x = ld128_dev(rp, (uint32_t)j * PB + 16u + (uint32_t)dp * 16u);
+                    op[i][0] = x.x; op[i][1] = x.y; op[i][2] = x.z; op[i][3] = x.w;
+                }
+            }
+        };
+        load_round(w);
+        // Selection is branch-free and the rare re-read loop is wave-uniform (all
+        // lanes run it, stale lanes take the new value).
+        uint32_t mv = ml.x, mt = ml.y, lv = ml.z, lt = ml.w;
+        for (int k = 0; k < POLL_MAX; ++k) {     // rare: stores still in flight
+            const bool need = in_s && !own && !(mt == tag && lt == tag);
+            if (__builtin_amdgcn_ballot_w64(need) == 0) break;
+            __builtin_amdgcn_s_sleep(2);
+            const u32x4 re = ld128_dev(rp, (uint32_t)jl * PB);
+            const uint32_t rmv = re.x, rmt = re.y, rlv = re.z, rlt = re.w;
+            mv = need ? rmv : mv;
+            mt = need ? rmt : mt;
+            lv = need ? rlv : lv;
+            lt = need ? rlt : lt;
+        }
+        good = good && (!in_s || own || (mt == tag && lt == tag));
+        const float own_m = s_own[q][D], own_l = s_own[q][D + 1];
+        const float mj = !in_s ? -__builtin_inff() : own ? own_m : __builtin_bit_cast(float, mv);
+        const float lj = !in_s ? 0.f : own ? own_l : __builtin_bit_cast(float, lv);
+        const float mx = wave_max(mj);
+        const float wj = fast_exp2(mj - mx);    // weight of split `lane` (0 past S)
+        lsum[q] = wave_sum(wj * lj);
+        float o0 = 0.f, o1 = 0.f;
+        for (int j0 = w; j0 < S; j0 += NW * R) {
+            if (j0 != w) load_round(j0);
+#pragma unroll
+            for (int i = 0; i < R; ++i) {
+                const int j = j0 + NW * i;       // wave-uniform
+                if (j >= S) break;
+                float v0, v1;
+                if (j == s) {                    // wave-uniform
+                    v0 = s_own[q][2 * dp];
+                    v1 = s_own[q][2 * dp + 1];
+                } else {
+                    uint32_t a0 = op[i][0], t0 = op[i][1], a1 = op[i][2], t1 = op[i][3];
+                    for (int k = 0; k < POLL_MAX; ++k) {
+                        const bool need = !(t0 == tag && t1 == tag);
+                        if (__builtin_amdgcn_ballot_w64(need) == 0) break;
+                        __builtin_amdgcn_s_sleep(2);
+                        const u32x4 re = ld128_dev(rp, (uint32_t)j * PB + 16u + (uint32_t)dp * 16u);
+                        const uint32_t ra0 = re.x, rt0 = re.y, ra1 = re.z, rt1 = re.w;
+                        a0 = need ? ra0 : a0;
+                        t0 = need ? rt0 : t0;
+                        a1 = need ? ra1 : a1;
+                        t1 = need ? rt1 : t1;
+                    }
+                    good = good && t0 == tag && t1 == tag;
+                    v0 = __builtin_bit_cast(float, a0);
+                    v1 = __builtin_bit_cast(float, a1);
+                }
+                const float f = __builtin_bit_cast(float,
+                    __builtin_amdgcn_readlane(__builtin_bit_cast(int, wj), j));
+                o0 = __builtin_fmaf(f, v0, o0);
+                o1 = __builtin_fmaf(f, v1, o1);
+            }
+        }
+        if (lane < D / 2) {
+            s_fold[q][w][2 * lane]     = o0;
+            s_fold[q][w][2 * lane + 1] = o1;
+        }
+    }
+    // A lost partial (never observed within the poll bound) shows as NaN.
+    if (__builtin_amdgcn_ballot_w64(!good) != 0 && lane == 0) s_bad = 1;
+    __syncthreads();
+    if (t < D) {
+#pragma unroll
+        for (int q = 0; q < QG; ++q) {
+            if (q >= rt.nq) break;
+            float o = 0.f;
+#pragma unroll
+            for (int v = 0; v < NW; ++v) o += s_fold[q][v][t];
+            const float r = lsum[q] == 0.f ? 0.f : o / lsum[q];
+            a.out[(size_t)(rt.oh0 + q) * D + t] = s_bad ? (uint16_t)0x7E00u : f2h_rne(r);
+        }
+    }
+    if (t == 0) {                            // every arrival is in: reset for the slot's next call
+        store_dev(ticket, 0u);
+        store_dev(ticket + 1, epoch + 1u);
+    }
+}
+
+} // namespace va

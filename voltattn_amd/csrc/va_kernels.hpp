@@ -7,40 +7,68 @@
 
 namespace va {
 
-// Arguments of the split-L decode pass (one work-group per (head, split)).
+// Arguments of the split-L decode pass: one work-group per (merge group,
+// split), a merge group being one (sequence b, KV head hk, query sub-group).
+// The reference's shape is B = 1, hkv = H, qgroup = 1, contiguous K/V.
 struct DecodeArgs {
-    const uint8_t*  k;      // payload [H][L][row bytes]
-    const uint8_t*  v;
-    const uint16_t* sk;     // fp16 scales [H][L][D/G] (quantized kinds)
+    const uint8_t*  k;      // payload: contiguous [hkv][L][row bytes], or the page pool
+    const uint8_t*  v;      //   [num_pages][hkv][page_rows][row bytes]
+    const uint16_t* sk;     // fp16 scales, same layouts with D/G per row (quantized kinds)
     const uint16_t* sv;
-    const uint16_t* q;      // fp16 [H][D]
-    float*          ws;     // [H*S][D+2]: (m, l, o[D]) per split, m in log2 units
+    const uint16_t* q;      // fp16 [B][hkv*qgroup][D]
+    float*          ws;     // [B*hkv*qgroup][S][D+2]: (m, l, o[D]) per split, m in log2 units
                             // (two-pass form only)
-    uint16_t*       out;    // fp16 [H][D], written by the fused merge
-    int   L, S, chunk;
+    uint16_t*       out;    // fp16 [B][hkv*qgroup][D], written by the fused merge
+    int   L, S, chunk;      // L: positions (paged form: max_seq_len); chunk: positions per split
     float qscale;           // log2(e) / sqrt(D)
     int   ticket_slot;      // >= 0: fused merge on this ticket slot; < 0: partials to ws
+    // grouped-query attention: query head (b, hk*qgroup + i) reads KV head hk
+    int   hkv;              // KV heads per sequence
+    int   qgroup;           // query heads per KV head
+    int   nsub;             // query sub-groups per KV head (ceil(qgroup / QG))
+    // paged form (block table over a page pool)
+    const int32_t* block_table;   // [B][max_pages] page ids
+    const int32_t* seq_lens;      // [B] positions per sequence
+    int   max_pages;        // block-table row length
+    int   page_shift;       // log2(page_rows)
+    int   num_pages;        // pages in the pool (ids outside [0, num_pages) are rejected)
 };
 
-// Fused second pass: per-(slot, head) ticket lines in static device memory
-// (zero at load): word 0 counts the arrivals of the head's work-groups, word 1
-// is the head's call epoch, advanced by the merging work-group. Calls rotate
-// over TICKET_SLOTS slots, so up to that many decode calls may be in flight on
-// one device at once. Each line is 256 bytes: atomics to one line serialize at
-// the memory side, and the S arrivals of every head land together.
-// The partials of a fused call live in library memory (PART_CAP partials of
-// PART_STRIDE 64-bit words per slot), not in the caller's ws. Calls with more
-// than TICKET_MAXH heads or more than PART_CAP partials use the two-pass form.
+// Fused second pass: per-(slot, merge group) ticket lines in static device
+// memory (zero at load): word 0 counts the arrivals of the group's
+// work-groups, word 1 is the group's call epoch, advanced by the merging
+// work-group. Calls rotate over TICKET_SLOTS slots, so up to that many decode
+// calls may be in flight on one device at once. Each line is 256 bytes: atomics
+// to one line serialize at the memory side, and the S arrivals of every group
+// land together. The partials of a fused call live in library memory (PART_CAP
+// partials of PART_STRIDE 64-bit words per slot), not in the caller's ws.
+// Calls with more than TICKET_MAXH merge groups, more than PART_CAP partials or
+// more than 64 splits use the two-pass form.
 constexpr int TICKET_SLOTS  = 16;
-constexpr int TICKET_MAXH   = 256;
+constexpr int TICKET_MAXH   = 1024;
 constexpr int TICKET_STRIDE = 64;   // uint32 per ticket line (256 bytes)
-constexpr int PART_CAP      = 1024; // partials (H*S) per slot
+constexpr int PART_CAP      = 2048; // partials (merge groups x QG x S) per slot
 constexpr int PART_STRIDE   = 130;  // 64-bit words per partial: m, l, o[D], D <= 128
+
+// Page ids of one split of the paged kernels are staged in LDS: a split may
+// span at most this many pages.
+constexpr int MAX_SPLIT_PAGES = 1024;
 
 // kind: 0 f16, 1 q8, 2 q4, 3 q3. tiled: the "+" kernels; otherwise the naive
 // one-position-per-wave kernels (f16, q8, q4 only).
 hipError_t launch_decode(int kind, bool tiled, int H, int D, int G,
                          const DecodeArgs& a, hipStream_t stream);
+
+// Grouped-query and paged forms of the tiled kernels (va_decode_ex.hip).
+// groups = merge groups (B * hkv * nsub); qg = query slots per work-group
+// (max_query_slots(kind) at most); paged selects the block-table form.
+hipError_t launch_decode_ex(int kind, int D, int G, int qg, bool paged, int groups,
+                            const DecodeArgs& a, hipStream_t stream);
+
+// Largest query-slot count (QG) a work-group of the kind carries, and the
+// work-group tile (positions per iteration) of the grouped/paged kernels.
+int max_query_slots(int kind);
+int tile_positions_ex(int kind, int D);
 
 // Work-groups per CU the split rule aims for (tiled kernels: the configured
 // groups per CU of the kind; naive kernels: 8).
@@ -61,6 +89,19 @@ hipError_t launch_probe(const void* src, size_t bytes, float* sink, int grid,
 // Bit-exact quantizer (bits 8/4/3) over rows of D fp32 values.
 hipError_t launch_quantize(int bits, int G, const float* x, size_t rows, int D,
                            uint8_t* packed, uint16_t* scales, hipStream_t stream);
+
+// Quantize-and-append of n new fp16 rows per (sequence, KV head) into a page
+// pool [num_pages][hkv][page_rows][row bytes] (+ fp16 scales [...][D/G]).
+struct AppendArgs {
+    const uint16_t* x;            // [B][hkv][n][D] fp16
+    const int32_t*  start;        // [B]: position of row 0 of each sequence
+    const int32_t*  block_table;  // [B][max_pages]
+    uint8_t*        pages;
+    uint16_t*       scales;
+    int B, hkv, n, D;
+    int page_rows, max_pages, num_pages;
+};
+hipError_t launch_append(int bits, int G, const AppendArgs& a, hipStream_t stream);
 
 // fp32 -> fp16 (round to nearest even) over n values.
 hipError_t launch_f32_to_f16(const float* x, size_t n, uint16_t* out, hipStream_t stream);

@@ -1,5 +1,7 @@
 // va_quant.hip — device-side producers of the decode path's inputs:
-//   * quantize_groups: the symmetric per-group quantizer + packer, bit-exact
+//   * quantize_groups / append_groups: the symmetric per-group quantizer +
+//     packer (over fp32 rows, or over fp16 rows written into a paged cache at
+//     given positions: the cache write path), bit-exact
 //     with the reference's host quantize() (src/voltattn.cu:705-745) for
 //     G in {32, 64}: amax in fp32, s = amax/lim (IEEE division), the fp16
 //     scale rounded to nearest even, codes clamp(rint(x / float(scale))), with
@@ -18,13 +20,66 @@ template <> struct QLim<8> { static constexpr int value = 127; };
 template <> struct QLim<4> { static constexpr int value = 7; };
 template <> struct QLim<3> { static constexpr int value = 3; };
 
+// Quantize and pack one group of G values (fp32 in registers) to `dst`
+// (G*BITS/8 bytes, 4-byte aligned) and its fp16 scale to `*scale`.
+template <int BITS, int G>
+__device__ __forceinline__ void quant_group(const float (&xv)[G], uint8_t* dst, uint16_t* scale) {
+    constexpr int lim = QLim<BITS>::value;
+    float amax = 0.f;
+#pragma unroll
+    for (int i = 0; i < G; ++i) amax = fmaxf(amax, __builtin_fabsf(xv[i]));
+    const float s = amax > 0.f ? amax / (float)lim : 1.f;
+    const uint16_t sb = f2h_rne(s);
+    const float sh = h2f(sb);
+    int code[G];
+#pragma unroll
+    for (int i = 0; i < G; ++i) {
+        const float t = xv[i] / sh;
+        int v = __builtin_isfinite(t) ? (int)__builtin_rintf(t) : 0;
+        v = v < -lim ? -lim : (v > lim ? lim : v);
+        code[i] = v;
+    }
+    *scale = sb;
+    uint32_t* d32 = reinterpret_cast<uint32_t*>(dst);
+    if constexpr (BITS == 8) {
+#pragma unroll
+        for (int k = 0; k < G / 4; ++k) {
+            uint32_t w = 0;
+#pragma unroll
+            for (int b = 0; b < 4; ++b) w |= (uint32_t)(uint8_t)(int8_t)code[4 * k + b] << (8 * b);
+            d32[k] = w;
+        }
+    } else if constexpr (BITS == 4) {             // element i: byte i/2, low nibble when i even
+#pragma unroll
+        for (int k = 0; k < G / 8; ++k) {
+            uint32_t w = 0;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) w |= (uint32_t)(code[8 * k + i] + 8) << (4 * i);
+            d32[k] = w;
+        }
+    } else {                                       // element i: bits [3i, 3i+3), little endian
+        constexpr int NW = 3 * G / 32;
+        uint32_t w[NW];
+#pragma unroll
+        for (int k = 0; k < NW; ++k) w[k] = 0;
+#pragma unroll
+        for (int i = 0; i < G; ++i) {
+            const uint32_t c = (uint32_t)(code[i] + 4);
+            const int b = 3 * i;
+            w[b / 32] |= c << (b % 32);
+            if (b % 32 > 29) w[b / 32 + 1] |= c >> (32 - b % 32);
+        }
+#pragma unroll
+        for (int k = 0; k < NW; ++k) d32[k] = w[k];
+    }
+}
+
 // One thread per quantization group of G consecutive elements. Groups are
 // contiguous: group r*(D/G) + g starts at element (r*(D/G) + g) * G.
 template <int BITS, int G>
 __global__ __launch_bounds__(256) void quantize_groups(const float* __restrict__ x, size_t ngroups,
                                                        uint8_t* __restrict__ packed,
                                                        uint16_t* __restrict__ scales) {
-    constexpr int lim = QLim<BITS>::value;
     const size_t stride = (size_t)gridDim.x * blockDim.x;
     for (size_t gi = (size_t)blockIdx.x * blockDim.x + threadIdx.x; gi < ngroups; gi += stride) {
         const f32x4* xp = reinterpret_cast<const f32x4*>(x + gi * G);
@@ -34,55 +89,68 @@ __global__ __launch_bounds__(256) void quantize_groups(const float* __restrict__
             const f32x4 w = xp[c];
             xv[4 * c] = w.x; xv[4 * c + 1] = w.y; xv[4 * c + 2] = w.z; xv[4 * c + 3] = w.w;
         }
-        float amax = 0.f;
+        quant_group<BITS, G>(xv, packed + gi * (G * BITS / 8), scales + gi);
+    }
+}
+
+// Destination row of (sequence b, KV head hk, position p) in a page pool
+// [num_pages][hkv][page_rows][...], or -1 when the position lies past the
+// block table or on a page id outside the pool (such rows are not written).
+__device__ __forceinline__ long long paged_row(const AppendArgs& a, int b, int hk, int p) {
+    if (p < 0) return -1;
+    const int pi = p / a.page_rows;
+    if (pi >= a.max_pages) return -1;
+    const int page = a.block_table[(size_t)b * a.max_pages + pi];
+    if (page < 0 || page >= a.num_pages) return -1;
+    return ((long long)page * a.hkv + hk) * a.page_rows + (p - pi * a.page_rows);
+}
+
+// Quantize-and-append: one thread per (b, hk, r, group) of the new rows
+// x[b][hk][r][D] (fp16), written at position start[b] + r.
+template <int BITS, int G>
+__global__ __launch_bounds__(256) void append_groups(AppendArgs a, size_t ngroups) {
+    const int NG = a.D / G;
+    const size_t stride = (size_t)gridDim.x * blockDim.x;
+    for (size_t gi = (size_t)blockIdx.x * blockDim.x + threadIdx.x; gi < ngroups; gi += stride) {
+        const int g = (int)(gi % NG);
+        size_t rest = gi / NG;
+        const int r = (int)(rest % a.n);
+        rest /= a.n;
+        const int hk = (int)(rest % a.hkv);
+        const int b  = (int)(rest / a.hkv);
+        const long long row = paged_row(a, b, hk, a.start[b] + r);
+        if (row < 0) continue;
+        const u32x4* xp = reinterpret_cast<const u32x4*>(a.x + gi * G);   // G fp16 values
+        float xv[G];
 #pragma unroll
-        for (int i = 0; i < G; ++i) amax = fmaxf(amax, __builtin_fabsf(xv[i]));
-        const float s = amax > 0.f ? amax / (float)lim : 1.f;
-        const uint16_t sb = f2h_rne(s);
-        const float sh = h2f(sb);
-        int code[G];
+        for (int c = 0; c < G / 8; ++c) {
+            const u32x4 w = xp[c];
 #pragma unroll
-        for (int i = 0; i < G; ++i) {
-            const float t = xv[i] / sh;
-            int v = __builtin_isfinite(t) ? (int)__builtin_rintf(t) : 0;
-            v = v < -lim ? -lim : (v > lim ? lim : v);
-            code[i] = v;
+            for (int k = 0; k < 4; ++k) {
+                xv[8 * c + 2 * k]     = h2f_lo(w[k]);
+                xv[8 * c + 2 * k + 1] = h2f_hi(w[k]);
+            }
         }
-        scales[gi] = sb;
-        if constexpr (BITS == 8) {
-            uint32_t* dst = reinterpret_cast<uint32_t*>(packed + gi * G);
-#pragma unroll
-            for (int k = 0; k < G / 4; ++k) {
-                uint32_t w = 0;
-#pragma unroll
-                for (int b = 0; b < 4; ++b) w |= (uint32_t)(uint8_t)(int8_t)code[4 * k + b] << (8 * b);
-                dst[k] = w;
-            }
-        } else if constexpr (BITS == 4) {         // element i: byte i/2, low nibble when i even
-            uint32_t* dst = reinterpret_cast<uint32_t*>(packed + gi * (G / 2));
-#pragma unroll
-            for (int k = 0; k < G / 8; ++k) {
-                uint32_t w = 0;
-#pragma unroll
-                for (int i = 0; i < 8; ++i) w |= (uint32_t)(code[8 * k + i] + 8) << (4 * i);
-                dst[k] = w;
-            }
-        } else {                                   // element i: bits [3i, 3i+3), little endian
-            constexpr int NW = 3 * G / 32;
-            uint32_t w[NW];
-#pragma unroll
-            for (int k = 0; k < NW; ++k) w[k] = 0;
-#pragma unroll
-            for (int i = 0; i < G; ++i) {
-                const uint32_t c = (uint32_t)(code[i] + 4);
-                const int b = 3 * i;
-                w[b / 32] |= c << (b % 32);
-                if (b % 32 > 29) w[b / 32 + 1] |= c >> (32 - b % 32);
-            }
-            uint32_t* dst = reinterpret_cast<uint32_t*>(packed + gi * (3 * G / 8));
-#pragma unroll
-            for (int k = 0; k < NW; ++k) dst[k] = w[k];
-        }
+        quant_group<BITS, G>(xv, a.pages + (size_t)row * (a.D * BITS / 8) + (size_t)g * (G * BITS / 8),
+                             a.scales + (size_t)row * NG + g);
+    }
+}
+
+// f16 append: one thread per 8 values (16 bytes) of the new rows.
+__global__ __launch_bounds__(256) void append_f16(AppendArgs a, size_t nchunks) {
+    const int CPR = a.D / 8;                       // 16-byte chunks per row
+    const size_t stride = (size_t)gridDim.x * blockDim.x;
+    for (size_t ci = (size_t)blockIdx.x * blockDim.x + threadIdx.x; ci < nchunks; ci += stride) {
+        const int c = (int)(ci % CPR);
+        size_t rest = ci / CPR;
+        const int r = (int)(rest % a.n);
+        rest /= a.n;
+        const int hk = (int)(rest % a.hkv);
+        const int b  = (int)(rest / a.hkv);
+        const long long row = paged_row(a, b, hk, a.start[b] + r);
+        if (row < 0) continue;
+        const u32x4 w = reinterpret_cast<const u32x4*>(a.x)[ci];
+        reinterpret_cast<u32x4*>(a.pages + (size_t)row * (a.D * 2))[c] = w;
     }
 }
 
@@ -148,6 +216,25 @@ hipError_t launch_quantize(int bits, int G, const float* x, size_t rows, int D, 
         if (bits == 8) VA_QLAUNCH(8, 64); else if (bits == 4) VA_QLAUNCH(4, 64); else VA_QLAUNCH(3, 64);
     }
 #undef VA_QLAUNCH
+    return hipGetLastError();
+}
+
+hipError_t launch_append(int bits, int G, const AppendArgs& a, hipStream_t stream) {
+    const size_t rows = (size_t)a.B * a.hkv * a.n;
+    if (bits == 16) {
+        const size_t nch = rows * (size_t)(a.D / 8);
+        hipLaunchKernelGGL(append_f16, dim3(grid_for(nch)), dim3(256), 0, stream, a, nch);
+        return hipGetLastError();
+    }
+    const size_t ngroups = rows * (size_t)(a.D / G);
+    const dim3 grid(grid_for(ngroups)), block(256);
+#define VA_ALAUNCH(B, GG) hipLaunchKernelGGL((append_groups<B, GG>), grid, block, 0, stream, a, ngroups)
+    if (G == 32) {
+        if (bits == 8) VA_ALAUNCH(8, 32); else if (bits == 4) VA_ALAUNCH(4, 32); else VA_ALAUNCH(3, 32);
+    } else {
+        if (bits == 8) VA_ALAUNCH(8, 64); else if (bits == 4) VA_ALAUNCH(4, 64); else VA_ALAUNCH(3, 64);
+    }
+#undef VA_ALAUNCH
     return hipGetLastError();
 }
 

@@ -89,7 +89,10 @@ std::atomic<unsigned> g_ticket_seq{0};
 // H*S <= PART_CAP), else the partials are left in ws for a separate merge pass.
 int run_splits(va_fmt fmt, const va_bufs* b, int H, int L, int D, int G, int S, void* stream,
                bool fused) {
-    va::DecodeArgs a;
+    va::DecodeArgs a{};
+    a.hkv = H;                    // the reference's shape: one query head per K/V head
+    a.qgroup = 1;
+    a.nsub = 1;
     a.k  = static_cast<const uint8_t*>(b->k);
     a.v  = static_cast<const uint8_t*>(b->v);
     a.sk = b->sk;
@@ -192,6 +195,263 @@ int va_merge(const float* ws, uint16_t* out, int H, int D, int S, void* stream) 
     if (!aligned(ws, 4) || !aligned(out, 2)) return fail(VA_EALIGN, "ws/out misaligned");
     const hipError_t e = va::launch_merge(ws, out, H, D, S, as_stream(stream));
     if (e != hipSuccess) return hip_fail(e, "merge launch");
+    return VA_OK;
+}
+
+} // extern "C"
+
+// ------------------------------------------ grouped-query / paged decode --
+namespace {
+
+bool pow2(int x) { return x > 0 && (x & (x - 1)) == 0; }
+int  log2i(int x) { int s = 0; while ((1 << s) < x) ++s; return s; }
+
+// Query slots per work-group (QG, a power of two) and sub-groups per KV head:
+// as few sub-groups as the kind's slot limit allows (each re-reads the rows),
+// then the smallest QG that covers the group.
+void pick_qg(int kind, int qgroup, int* qg, int* nsub) {
+    const int qmax = va::max_query_slots(kind);
+    const int ns = (qgroup + qmax - 1) / qmax;
+    const int per = (qgroup + ns - 1) / ns;
+    int q = 1;
+    while (q < per) q <<= 1;
+    *qg = q;
+    *nsub = ns;
+}
+
+// Split count and split length for `groups` merge groups over sequences of up
+// to max_len positions: one 4-wave work-group per CU, splits of whole kernel
+// tiles, at most 64 splits (the fused merge's limit). S_req > 0 fixes S.
+void splits_ex(int kind, int D, int groups, int max_len, int S_req, int* S, int* chunk) {
+    int cus = cu_count();
+    if (cus <= 0) cus = 256;
+    const int tb = va::tile_positions_ex(kind, D);
+    const int tiles = std::max(1, (max_len + tb - 1) / tb);
+    int s0 = S_req;
+    if (s0 <= 0) s0 = std::max(1, std::min(std::min(tiles, 64), (cus + groups - 1) / groups));
+    const int tps = (tiles + s0 - 1) / s0;
+    *chunk = tps * tb;
+    *S = S_req > 0 ? S_req : std::max(1, (max_len + *chunk - 1) / *chunk);
+}
+
+bool fused_ok(int groups, int qg, int S) {
+    return S <= 64 && groups <= va::TICKET_MAXH && (long long)groups * qg * S <= va::PART_CAP;
+}
+
+int launch_ex(va_fmt fmt, va::DecodeArgs& a, int D, int G, int qg, bool paged, int groups,
+              int heads_total, void* stream) {
+    const bool fused = fused_ok(groups, qg, a.S);
+    a.ticket_slot = fused ? (int)(g_ticket_seq.fetch_add(1u) % va::TICKET_SLOTS) : -1;
+    a.qscale = (float)(1.4426950408889634074 / std::sqrt((double)D));
+    hipError_t e = va::launch_decode_ex(kind_of(fmt), D, is_f16(fmt) ? 64 : G, qg, paged, groups, a,
+                                        as_stream(stream));
+    if (e != hipSuccess) return hip_fail(e, "decode launch");
+    if (!fused) {
+        e = va::launch_merge(a.ws, a.out, heads_total, D, a.S, as_stream(stream));
+        if (e != hipSuccess) return hip_fail(e, "merge launch");
+    }
+    return VA_OK;
+}
+
+} // namespace
+
+extern "C" {
+
+int va_pick_splits_gqa(va_fmt fmt, int Hq, int Hkv, int L, int D, int* S) {
+    if (!S) return fail(VA_ENULL, "S is NULL");
+    if (!valid_fmt(fmt) || Hq < 1 || Hkv < 1 || Hq % Hkv || L < 1 || (D != 64 && D != 128))
+        return fail(VA_EINVAL, "invalid arguments to va_pick_splits_gqa");
+    if (Hq == Hkv) return va_pick_splits(fmt, Hq, L, D, S);
+    if (!tiled_of(fmt)) return fail(VA_EINVAL, "grouped-query decode needs a tiled format (f16+, q8+, q4+, q3+)");
+    int qg, nsub, chunk;
+    pick_qg(kind_of(fmt), Hq / Hkv, &qg, &nsub);
+    splits_ex(kind_of(fmt), D, Hkv * nsub, L, 0, S, &chunk);
+    return VA_OK;
+}
+
+int va_decode_gqa(va_fmt fmt, const va_bufs* b, int Hq, int Hkv, int L, int D, int G, int S,
+                  void* stream) {
+    if (!valid_fmt(fmt)) return fail(VA_EINVAL, "invalid format %d", (int)fmt);
+    if (Hq < 1 || Hkv < 1 || Hq % Hkv)
+        return fail(VA_EINVAL, "Hq must be a positive multiple of Hkv (Hq=%d, Hkv=%d)", Hq, Hkv);
+    if (S < 0) return fail(VA_EINVAL, "S must be >= 0 (0 picks it)");
+    if (Hq == Hkv) {
+        int s = S;
+        if (s == 0) {
+            const int rc = va_pick_splits(fmt, Hq, L, D, &s);
+            if (rc) return rc;
+        }
+        return va_decode(fmt, b, Hq, L, D, G, s, stream);
+    }
+    if (!tiled_of(fmt)) return fail(VA_EINVAL, "grouped-query decode needs a tiled format (f16+, q8+, q4+, q3+)");
+    int rc = validate(fmt, b, Hkv, L, D, G, 1, true);
+    if (rc) return rc;
+    int qg, nsub, Sx, chunk;
+    pick_qg(kind_of(fmt), Hq / Hkv, &qg, &nsub);
+    const int groups = Hkv * nsub;
+    splits_ex(kind_of(fmt), D, groups, L, S, &Sx, &chunk);
+    if ((long long)Hq * Sx > 0x7FFFFFFFLL || (long long)groups * Sx > 0x7FFFFFFFLL)
+        return fail(VA_ERANGE, "Hq*S too large");
+    va::DecodeArgs a{};
+    a.k = static_cast<const uint8_t*>(b->k);
+    a.v = static_cast<const uint8_t*>(b->v);
+    a.sk = b->sk;
+    a.sv = b->sv;
+    a.q = b->q;
+    a.ws = b->ws;
+    a.out = b->out;
+    a.L = L;
+    a.S = Sx;
+    a.chunk = chunk;
+    a.hkv = Hkv;
+    a.qgroup = Hq / Hkv;
+    a.nsub = nsub;
+    return launch_ex(fmt, a, D, G, qg, false, groups, Hq, stream);
+}
+
+size_t va_page_bytes(va_fmt fmt, int Hkv, int page_rows, int D) {
+    if (!valid_fmt(fmt) || Hkv < 1 || page_rows < 1 || D < 1) return 0;
+    return (size_t)Hkv * page_rows * row_bytes(fmt, D);
+}
+
+size_t va_page_scale_bytes(va_fmt fmt, int Hkv, int page_rows, int D, int G) {
+    if (!valid_fmt(fmt) || is_f16(fmt) || Hkv < 1 || page_rows < 1 || G < 1 || D % G) return 0;
+    return (size_t)Hkv * page_rows * (D / G) * 2;
+}
+
+} // extern "C"
+
+namespace {
+
+int validate_shape(va_fmt fmt, const va_paged_shape* sh, bool decode) {
+    if (!valid_fmt(fmt)) return fail(VA_EINVAL, "invalid format %d", (int)fmt);
+    if (!sh) return fail(VA_ENULL, "shape is NULL");
+    if (sh->B < 1 || sh->Hkv < 1) return fail(VA_EINVAL, "B and Hkv must be >= 1");
+    if (sh->D != 64 && sh->D != 128) return fail(VA_EINVAL, "D must be 64 or 128 (got %d)", sh->D);
+    if (!is_f16(fmt) && !((sh->G == 32 || sh->G == 64) && sh->G <= sh->D))
+        return fail(VA_EINVAL, "G must be 32 or 64 and <= D (got G=%d)", sh->G);
+    if (sh->max_pages < 1 || sh->num_pages < 1) return fail(VA_EINVAL, "max_pages and num_pages must be >= 1");
+    if (sh->page_rows < 1) return fail(VA_EINVAL, "page_rows must be >= 1");
+    if ((long long)sh->num_pages * sh->Hkv * sh->page_rows > (1LL << 40))
+        return fail(VA_ERANGE, "page pool too large");
+    if (!decode) return VA_OK;
+    if (!tiled_of(fmt)) return fail(VA_EINVAL, "paged decode needs a tiled format (f16+, q8+, q4+, q3+)");
+    if (sh->Hq < 1 || sh->Hq % sh->Hkv)
+        return fail(VA_EINVAL, "Hq must be a positive multiple of Hkv (Hq=%d, Hkv=%d)", sh->Hq, sh->Hkv);
+    if (!pow2(sh->page_rows) || sh->page_rows < 64 || sh->page_rows > (1 << 24))
+        return fail(VA_EINVAL, "page_rows must be a power of two in [64, 2^24] (got %d)", sh->page_rows);
+    if (sh->max_seq_len < 0 || (long long)sh->max_seq_len > (long long)sh->max_pages * sh->page_rows)
+        return fail(VA_EINVAL, "max_seq_len must be in [0, max_pages*page_rows]");
+    if ((long long)sh->max_pages * sh->page_rows > 0x7FFFFFFFLL)
+        return fail(VA_ERANGE, "max_pages*page_rows must stay below 2^31");
+    return VA_OK;
+}
+
+} // namespace
+
+extern "C" {
+
+int va_pick_splits_paged(va_fmt fmt, const va_paged_shape* sh, int* S) {
+    if (!S) return fail(VA_ENULL, "S is NULL");
+    int rc = validate_shape(fmt, sh, true);
+    if (rc) return rc;
+    int qg, nsub, chunk;
+    pick_qg(kind_of(fmt), sh->Hq / sh->Hkv, &qg, &nsub);
+    splits_ex(kind_of(fmt), sh->D, sh->B * sh->Hkv * nsub, std::max(1, sh->max_seq_len), 0, S, &chunk);
+    // a split may span at most MAX_SPLIT_PAGES pages
+    while ((chunk / sh->page_rows) + 2 > va::MAX_SPLIT_PAGES && *S < 0x7FFF) {
+        splits_ex(kind_of(fmt), sh->D, sh->B * sh->Hkv * nsub, std::max(1, sh->max_seq_len), *S * 2, S, &chunk);
+    }
+    return VA_OK;
+}
+
+int va_decode_paged(va_fmt fmt, const va_paged_bufs* b, const va_paged_shape* sh, int S,
+                    void* stream) {
+    int rc = validate_shape(fmt, sh, true);
+    if (rc) return rc;
+    if (!b) return fail(VA_ENULL, "bufs is NULL");
+    if (S < 0) return fail(VA_EINVAL, "S must be >= 0 (0 picks it)");
+    const bool quant = !is_f16(fmt);
+    if (!b->k || !b->v || !b->q || !b->out || !b->ws || !b->block_table || !b->seq_lens)
+        return fail(VA_ENULL, "k, v, q, out, ws, block_table and seq_lens must be non-NULL");
+    if (quant && (!b->sk || !b->sv)) return fail(VA_ENULL, "quantized formats need sk and sv");
+    const size_t kal = kind_of(fmt) == 3 ? 4 : 16;
+    if (!aligned(b->k, kal) || !aligned(b->v, kal))
+        return fail(VA_EALIGN, "k and v must be %zu-byte aligned", kal);
+    if (!aligned(b->q, 16)) return fail(VA_EALIGN, "q must be 16-byte aligned");
+    if (!aligned(b->out, 2) || !aligned(b->ws, 4) || !aligned(b->block_table, 4) || !aligned(b->seq_lens, 4))
+        return fail(VA_EALIGN, "out, ws, block_table or seq_lens misaligned");
+    if (quant) {
+        const size_t sal = (sh->D / sh->G) >= 2 ? 4 : 2;
+        if (!aligned(b->sk, sal) || !aligned(b->sv, sal))
+            return fail(VA_EALIGN, "sk and sv must be %zu-byte aligned", sal);
+    }
+    int qg, nsub, Sx, chunk;
+    pick_qg(kind_of(fmt), sh->Hq / sh->Hkv, &qg, &nsub);
+    const long long groups = (long long)sh->B * sh->Hkv * nsub;
+    if (S == 0) {
+        rc = va_pick_splits_paged(fmt, sh, &Sx);
+        if (rc) return rc;
+        S = Sx;
+    }
+    splits_ex(kind_of(fmt), sh->D, (int)std::min<long long>(groups, 1 << 30), std::max(1, sh->max_seq_len), S,
+              &Sx, &chunk);
+    if (chunk / sh->page_rows + 2 > va::MAX_SPLIT_PAGES)
+        return fail(VA_EINVAL, "a split of %d positions spans more than %d pages; raise S", chunk,
+                    va::MAX_SPLIT_PAGES);
+    if (groups * Sx > 0x7FFFFFFFLL || (long long)sh->B * sh->Hq * Sx > 0x7FFFFFFFLL)
+        return fail(VA_ERANGE, "B*Hq*S too large");
+    va::DecodeArgs a{};
+    a.k = static_cast<const uint8_t*>(b->k);
+    a.v = static_cast<const uint8_t*>(b->v);
+    a.sk = b->sk;
+    a.sv = b->sv;
+    a.q = b->q;
+    a.ws = b->ws;
+    a.out = b->out;
+    a.L = sh->max_seq_len;           // the paged kernels' length cap
+    a.S = Sx;
+    a.chunk = chunk;
+    a.hkv = sh->Hkv;
+    a.qgroup = sh->Hq / sh->Hkv;
+    a.nsub = nsub;
+    a.block_table = b->block_table;
+    a.seq_lens = b->seq_lens;
+    a.max_pages = sh->max_pages;
+    a.page_shift = log2i(sh->page_rows);
+    a.num_pages = sh->num_pages;
+    return launch_ex(fmt, a, sh->D, sh->G, qg, true, (int)groups, sh->B * sh->Hq, stream);
+}
+
+int va_append_kv(va_fmt fmt, const uint16_t* x, int n, const int32_t* start,
+                 const int32_t* block_table, const va_paged_shape* sh, void* pages,
+                 uint16_t* scales, void* stream) {
+    int rc = validate_shape(fmt, sh, false);
+    if (rc) return rc;
+    if (n < 0) return fail(VA_EINVAL, "n must be >= 0");
+    if (n == 0) return VA_OK;
+    const bool quant = !is_f16(fmt);
+    if (!x || !start || !block_table || !pages || (quant && !scales))
+        return fail(VA_ENULL, "x, start, block_table, pages (and scales) must be non-NULL");
+    if (!aligned(x, 16)) return fail(VA_EALIGN, "x must be 16-byte aligned");
+    if (!aligned(pages, quant ? 4 : 16)) return fail(VA_EALIGN, "pages misaligned");
+    if (quant && !aligned(scales, 2)) return fail(VA_EALIGN, "scales must be 2-byte aligned");
+    if (!aligned(start, 4) || !aligned(block_table, 4)) return fail(VA_EALIGN, "start/block_table misaligned");
+    va::AppendArgs a{};
+    a.x = x;
+    a.start = start;
+    a.block_table = block_table;
+    a.pages = static_cast<uint8_t*>(pages);
+    a.scales = scales;
+    a.B = sh->B;
+    a.hkv = sh->Hkv;
+    a.n = n;
+    a.D = sh->D;
+    a.page_rows = sh->page_rows;
+    a.max_pages = sh->max_pages;
+    a.num_pages = sh->num_pages;
+    const hipError_t e = va::launch_append(bits_of(fmt), is_f16(fmt) ? 32 : sh->G, a, as_stream(stream));
+    if (e != hipSuccess) return hip_fail(e, "append launch");
     return VA_OK;
 }
 

@@ -1,0 +1,346 @@
+// va_tiled.hpp — the tiled ("+") split-L decode kernel, shared by the
+// reference-shape launches (va_decode.hip) and the grouped-query / paged
+// launches (va_decode_ex.hip).
+//
+// One work-group of WAVES wave64 per (merge group, split) computes log-sum-exp
+// partials (m, l, o[D]) over positions [s*chunk, min(L, (s+1)*chunk)) of one
+// KV head, for QG query heads that share it (flash-decoding; reference
+// src/voltattn.cu:80-120, 364-649, which has QG = 1 and contiguous K/V).
+// Each lane takes LB = 16 contiguous bytes (12 for q3) of a row with one
+// buffer load, so one wave-wide load instruction covers PPW = 64/LP rows with
+// no gaps; each row is unpacked once into exact fp16 pairs (va_codec.hpp) and
+// used by all QG query heads, the partial dot is summed over the LP lanes with
+// DPP row ops, and the online softmax runs in fp32 in log2 units (q is
+// pre-scaled by log2(e)/sqrt(D), exponentials are v_exp_f32). Per wave and
+// iteration U rows per lane are in flight for K and V, and the next tile is
+// prefetched into registers while the current one is computed. The fp16 group
+// scales of a wave's tile are fetched with one coalesced load per tensor and
+// staged once in LDS as (k, v) pairs.
+//
+// The running maximum of each query head is shared by the whole wave and is
+// raised lazily: a rescale (one cross-lane max and a multiply of l and o)
+// happens only when a new score exceeds it by more than RESCALE_SLACK (log2
+// units), so weights stay <= 2^RESCALE_SLACK and most tiles skip the rescale
+// entirely. (o, l, m) always describe the same normalised value, so the
+// result is unchanged.
+//
+// Contiguous form (PAGED = false): K/V rows of KV head hk are [hk][L][row];
+// each work-group builds raw buffer resources covering exactly its split, so a
+// load at or past the split end returns 0 with no memory access (partial
+// tiles, and the prefetch beyond the last tile).
+//
+// Paged form: rows of sequence b live in pages of 2^page_shift rows, page p
+// holding [hkv][page_rows][row] of the pool; position j of sequence b is row
+// j mod page_rows of page block_table[b][j / page_rows]. Page sizes are
+// multiples of the wave tile TW and splits start on work-group tiles, so every
+// wave tile lies in one page; each wave tile gets its own buffer resources,
+// clamped to the split (no access past it, so the prefetch beyond the last
+// tile reads nothing, as in the contiguous form) and empty for a page id
+// outside the pool (which also marks the output NaN). The page ids of a split
+// are staged in LDS once.
+#pragma once
+#include "va_codec.hpp"
+#include "va_fused.hpp"
+
+namespace va {
+
+constexpr float RESCALE_SLACK = 8.0f;    // log2 units: weights stay <= 256
+constexpr float M_INIT = -1e30f;         // finite "no score yet" maximum
+
+template <int KIND, int D, int G, int U, int WAVES, int QG, bool PAGED>
+__global__ __launch_bounds__(WAVES * 64) void decode_tiled(DecodeArgs a) {
+    using T = Tile<KIND, D>;
+    using C = Codec<KIND>;
+    using LoadT = typename LaneLoad<KIND>::type;
+    constexpr int ROWB = T::ROWB, LB = T::LB, LP = T::LP, PPW = T::PPW, EPL = T::EPL, NP = C::NP;
+    static_assert(EPL == C::EPL, "codec width");
+    constexpr bool QUANT = KIND != KF16;
+    constexpr int NG  = D / G;                   // scale groups per row
+    constexpr int TW  = PPW * U;                 // rows per wave per iteration
+    constexpr int TB  = TW * WAVES;              // rows per work-group per iteration
+    constexpr int SCN = QUANT ? TW * NG : 1;     // (k, v) scale pairs per wave tile
+    constexpr int SCE = !QUANT ? 1 : NG >= 2 ? SCN / 2 : SCN;  // scale dwords/halves per tensor
+    constexpr int SCR = (SCE + 63) / 64;         // scale loads per lane per tensor
+    static_assert(!QUANT || G % EPL == 0, "a lane's elements share one scale group");
+    static_assert(SCE % 64 == 0 || SCR == 1, "scale entries fill whole wave loads");
+
+    __shared__ uint32_t s_scale[WAVES][SCN];
+    __shared__ float    s_red[QG][WAVES * 4][D + 1];
+    __shared__ float    s_l[QG][WAVES * 4];
+    __shared__ float    s_m[QG][WAVES];
+    __shared__ int      s_page[PAGED ? MAX_SPLIT_PAGES : 1];
+
+    // ---- work-group -> (sequence b, KV head hk, query sub-group, split s)
+    Route rt;
+    rt.mg = (int)blockIdx.x / a.S;
+    rt.s  = (int)blockIdx.x - rt.mg * a.S;
+    int b = 0, hk = rt.mg, sub = 0;
+    if constexpr (QG > 1 || PAGED) {
+        sub = rt.mg % a.nsub;
+        const int r = rt.mg / a.nsub;
+        hk = r % a.hkv;
+        b  = r / a.hkv;
+    }
+    if constexpr (QG == 1 && !PAGED) {           // the reference's shape: head = merge group
+        rt.nq  = 1;
+        rt.oh0 = rt.mg;
+    } else {
+        rt.nq  = min(QG, a.qgroup - sub * QG);
+        rt.oh0 = (b * a.hkv + hk) * a.qgroup + sub * QG;
+    }
+    const int s = rt.s;
+    const unsigned epoch = read_epoch(a, rt.mg);
+    const int wave = uniform((int)(threadIdx.x >> 6));
+    const int lane = (int)(threadIdx.x & 63);
+    const int sl   = lane % LP;                  // lane within its row
+    const int pw   = lane / LP;                  // row slot within a wave load
+    const int grp  = (sl * EPL) / G;             // scale group of this lane
+
+    int L = a.L;
+    bool bad = false;                            // invalid input: the output becomes NaN
+    if constexpr (PAGED) {
+        const int cap = min(a.L, min(a.S * a.chunk, a.max_pages << a.page_shift));
+        L = a.seq_lens[b];
+        if (L > cap) { bad = true; L = cap; }
+        L = max(L, 0);
+    }
+    const int j0 = s * a.chunk;
+    const int n  = min(L - j0, a.chunk);         // rows of this split (<= 0: empty)
+
+    float m[QG], l[QG];
+    float o[QG][EPL];
+#pragma unroll
+    for (int q = 0; q < QG; ++q) {
+        m[q] = M_INIT;
+        l[q] = 0.f;
+#pragma unroll
+        for (int e = 0; e < EPL; ++e) o[q][e] = 0.f;
+    }
+
+    if (n > 0) {
+        const uint32_t lane_off = (uint32_t)(pw * ROWB + sl * LB);
+        const int niter = (n + TB - 1) / TB;
+
+        // Contiguous form: resources over the split, tile offsets in soffset
+        // (the paged form builds per-tile resources and leaves these empty).
+        const size_t   row0  = PAGED ? 0 : (size_t)hk * a.L + j0;
+        const uint32_t nsplt = PAGED ? 0u : (uint32_t)n;
+        const __amdgpu_buffer_rsrc_t rk = make_rsrc(a.k + row0 * ROWB, nsplt * ROWB);
+        const __amdgpu_buffer_rsrc_t rv = make_rsrc(a.v + row0 * ROWB, nsplt * ROWB);
+        const __amdgpu_buffer_rsrc_t rsk = QUANT ? make_rsrc(a.sk + row0 * NG, nsplt * NG * 2) : rk;
+        const __amdgpu_buffer_rsrc_t rsv = QUANT ? make_rsrc(a.sv + row0 * NG, nsplt * NG * 2) : rv;
+        int p0 = 0;
+        if constexpr (PAGED) {
+            // Stage the split's page ids (its positions span pages p0 .. p1).
+            p0 = j0 >> a.page_shift;
+            const int np = ((j0 + n - 1) >> a.page_shift) - p0 + 1;
+            const int32_t* tab = a.block_table + (size_t)b * a.max_pages + p0;
+            for (int i = (int)threadIdx.x; i < np; i += WAVES * 64) s_page[i] = tab[i];
+            __syncthreads();
+        }
+
+        // Two register stages (A, B) alternate: while one tile is computed the
+        // next one is already in flight, and no register copy ever waits on it.
+        LoadT ka[U], va_[U], kb[U], vb[U];
+        uint32_t ska[SCR], sva[SCR], skb[SCR], svb[SCR];
+
+        // Issue order is pinned (scales, then K, then V) so the prologue and the
+        // loop leave the same pending-load sequence and the waits stay partial.
+        auto load_tile = [&](int it, LoadT* kk, LoadT* vv, uint32_t* sk, uint32_t* sv) {
+            const int t0 = it * TB + wave * TW;                 // tile's first row in the split
+            __amdgpu_buffer_rsrc_t tk = rk, tv = rv, tsk = rsk, tsv = rsv;
+            uint32_t soff = (uint32_t)t0;
+            if constexpr (PAGED) {
+                // Each wave tile lies in one page (TW divides the page size).
+                const int pos  = j0 + t0;                       // position in the sequence
+                const int rows = max(0, min(TW, n - t0));       // rows of this tile inside the split
+                int page = 0;
+                if (rows > 0) page = uniform(s_page[(pos >> a.page_shift) - p0]);
+                const bool ok = page >= 0 && page < a.num_pages;
+                bad = bad || (rows > 0 && !ok);
+                const uint32_t nrow = ok ? (uint32_t)rows : 0u;
+                const size_t row = ((size_t)(ok ? page : 0) * a.hkv + hk) * ((size_t)1 << a.page_shift) +
+                                   (size_t)(pos & ((1 << a.page_shift) - 1));
+                tk = make_rsrc(a.k + row * ROWB, nrow * ROWB);
+                tv = make_rsrc(a.v + row * ROWB, nrow * ROWB);
+                if constexpr (QUANT) {
+                    tsk = make_rsrc(a.sk + row * NG, nrow * NG * 2);
+                    tsv = make_rsrc(a.sv + row * NG, nrow * NG * 2);
+                }
+                soff = 0;
+            }
+            const uint32_t tpos = sgpr(soff);                   // wave-uniform
+            __builtin_amdgcn_sched_barrier(0);
+            if constexpr (QUANT) {            // lanes past SCE repeat the last entry (unused)
+#pragma unroll
+                for (int r = 0; r < SCR; ++r) {
+                    const uint32_t sidx = (uint32_t)min(lane + 64 * r, SCE - 1);
+                    if constexpr (NG >= 2) {
+                        sk[r] = ld32(tsk, sidx * 4, tpos * NG * 2);
+                        sv[r] = ld32(tsv, sidx * 4, tpos * NG * 2);
+                    } else {
+                        sk[r] = ld16(tsk, sidx * 2, tpos * 2);
+                        sv[r] = ld16(tsv, sidx * 2, tpos * 2);
+                    }
+                }
+            }
+#pragma unroll
+            for (int u = 0; u < U; ++u)
+                kk[u] = lane_load<KIND>(tk, lane_off + (uint32_t)(u * PPW * ROWB), tpos * ROWB);
+#pragma unroll
+            for (int u = 0; u < U; ++u)
+                vv[u] = lane_load<KIND>(tv, lane_off + (uint32_t)(u * PPW * ROWB), tpos * ROWB);
+            __builtin_amdgcn_sched_barrier(0);
+        };
+
+        // The first tile is issued before q is read, so the two latencies overlap.
+        load_tile(0, ka, va_, ska, sva);
+
+        // q slices of this lane (dims [sl*EPL, sl*EPL + EPL)) in codec form;
+        // query slots past nq read query slot 0 (their results are dropped).
+        typename C::QReg qr[QG];
+#pragma unroll
+        for (int q = 0; q < QG; ++q)
+            C::load_q(qr[q], a.q + (size_t)(rt.oh0 + (q < rt.nq ? q : 0)) * D + sl * EPL, a.qscale);
+        const uint32_t magic = C::magic();
+
+        auto stage_scales = [&](const uint32_t* sk, const uint32_t* sv) {  // (k | v << 16) pairs
+            if constexpr (QUANT) {
+#pragma unroll
+                for (int r = 0; r < SCR; ++r) {
+                    const int e = lane + 64 * r;
+                    if (e < SCE) {
+                        if constexpr (NG >= 2) {
+                            s_scale[wave][2 * e]     = __builtin_amdgcn_perm(sv[r], sk[r], 0x05040100u);
+                            s_scale[wave][2 * e + 1] = __builtin_amdgcn_perm(sv[r], sk[r], 0x07060302u);
+                        } else {
+                            s_scale[wave][e] = (sk[r] & 0xFFFFu) | (sv[r] << 16);
+                        }
+                    }
+                }
+            }
+        };
+
+        auto compute_tile = [&](int it, const LoadT* kk, const LoadT* vv) {
+            const int rem = uniform(n - it * TB - wave * TW);   // valid rows of this wave tile
+            float sc[QG][U];
+            uint32_t pair[U];
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                const int slot = u * PPW + pw;
+                h2 pk[NP];
+                C::unpack(kk[u], magic, pk);
+                float ks = 1.f;
+                pair[u] = 0;
+                if constexpr (QUANT) {
+                    pair[u] = s_scale[wave][slot * NG + grp];
+                    ks = h2f_lo(pair[u]);
+                }
+#pragma unroll
+                for (int q = 0; q < QG; ++q) {
+                    float d = C::dot(pk, qr[q]);
+                    if constexpr (QUANT) d *= ks;
+                    d = group_sum<LP>(d);
+                    sc[q][u] = slot < rem ? d : -__builtin_inff();
+                }
+            }
+#pragma unroll
+            for (int q = 0; q < QG; ++q) {
+                float tmax = sc[q][0];
+#pragma unroll
+                for (int u = 1; u < U; ++u) tmax = fmaxf(tmax, sc[q][u]);
+                if (__builtin_amdgcn_ballot_w64(tmax > m[q] + RESCALE_SLACK)) {
+                    const float mn = uniformf(wave_max(fmaxf(m[q], tmax)));
+                    const float c  = fast_exp2(m[q] - mn);
+                    l[q] *= c;
+#pragma unroll
+                    for (int e = 0; e < EPL; ++e) o[q][e] *= c;
+                    m[q] = mn;
+                }
+            }
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                h2 pv[NP];
+                C::unpack(vv[u], magic, pv);
+#pragma unroll
+                for (int q = 0; q < QG; ++q) {
+                    const float p = fast_exp2(sc[q][u] - m[q]);
+                    l[q] += p;
+                    float ev = p;
+                    if constexpr (QUANT) ev = p * h2f_hi(pair[u]);
+                    C::axpy(pv, ev, o[q]);
+                }
+            }
+        };
+
+        // Tiles are processed in pairs. Loads past the end of the split return
+        // zeros without memory traffic and their scores are masked, so the
+        // prefetch after the last tile and the empty tile that completes an
+        // odd count add no traffic and leave (m, l, o) unchanged.
+        const int npair = (niter + 1) / 2;
+        for (int ip = 0; ip < npair; ++ip) {
+            const int it = 2 * ip;
+            stage_scales(ska, sva);
+            load_tile(it + 1, kb, vb, skb, svb);
+            compute_tile(it, ka, va_);
+            stage_scales(skb, svb);
+            load_tile(it + 2, ka, va_, ska, sva);
+            compute_tile(it + 1, kb, vb);
+        }
+#pragma unroll
+        for (int q = 0; q < QG; ++q) C::finish(o[q]);
+    }
+
+    // ---- work-group merge: slots of a DPP row first, then rows/waves via LDS.
+#pragma unroll
+    for (int q = 0; q < QG; ++q) {
+#pragma unroll
+        for (int off = LP; off < 16; off *= 2) {
+            if (off == 1) { l[q] += dpp<dpp_row_ror(1)>(l[q]); for (int e = 0; e < EPL; ++e) o[q][e] += dpp<dpp_row_ror(1)>(o[q][e]); }
+            if (off == 2) { l[q] += dpp<dpp_row_ror(2)>(l[q]); for (int e = 0; e < EPL; ++e) o[q][e] += dpp<dpp_row_ror(2)>(o[q][e]); }
+            if (off == 4) { l[q] += dpp<dpp_row_ror(4)>(l[q]); for (int e = 0; e < EPL; ++e) o[q][e] += dpp<dpp_row_ror(4)>(o[q][e]); }
+            if (off == 8) { l[q] += dpp<dpp_row_ror(8)>(l[q]); for (int e = 0; e < EPL; ++e) o[q][e] += dpp<dpp_row_ror(8)>(o[q][e]); }
+        }
+    }
+    const int row = lane >> 4;
+    if ((lane & 15) < LP) {                       // one slot per 16-lane row holds the row sum
+#pragma unroll
+        for (int q = 0; q < QG; ++q) {
+#pragma unroll
+            for (int e = 0; e < EPL; ++e) s_red[q][wave * 4 + row][sl * EPL + e] = o[q][e];
+            if (sl == 0) s_l[q][wave * 4 + row] = l[q];
+        }
+    }
+    if (lane == 0) {
+#pragma unroll
+        for (int q = 0; q < QG; ++q) s_m[q][wave] = m[q];
+    }
+    // A bad tile in any wave marks every partial of the group (l = NaN).
+    bool any_bad = false;
+    if constexpr (PAGED) any_bad = __syncthreads_or(bad);
+    else __syncthreads();
+    const int t = (int)threadIdx.x;
+    float M[QG], acc[QG], ls[QG];
+#pragma unroll
+    for (int q = 0; q < QG; ++q) {
+        M[q] = 0.f;
+        acc[q] = 0.f;
+        ls[q] = 0.f;
+        if (t < D) {
+            M[q] = s_m[q][0];
+#pragma unroll
+            for (int w = 1; w < WAVES; ++w) M[q] = fmaxf(M[q], s_m[q][w]);
+            float f[WAVES];
+#pragma unroll
+            for (int w = 0; w < WAVES; ++w) f[w] = fast_exp2(s_m[q][w] - M[q]);
+#pragma unroll
+            for (int r = 0; r < WAVES * 4; ++r) acc[q] = __builtin_fmaf(f[r / 4], s_red[q][r][t], acc[q]);
+#pragma unroll
+            for (int r = 0; r < WAVES * 4; ++r) ls[q] = __builtin_fmaf(f[r / 4], s_l[q][r], ls[q]);
+            if (any_bad) ls[q] = __builtin_nanf("");
+        }
+    }
+    finish_partial<D, WAVES * 64, QG>(a, rt, M, ls, acc, epoch);
+}
+
+} // namespace va
