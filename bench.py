@@ -23,8 +23,10 @@ Method (reference bench, src/voltattn.cu:967-1070, re-derived for MI355X):
     plus the reference's best-of-K single-launch time, each launch preceded by
     an untimed one so the start event is stamped when the GPU is already busy;
   * roofline: algorithmic bytes per decode-kernel launch (compressed K+V
-    payload + fp16 scales: 2*H*L*(D*b/8 + 2*D/G)) over the decode kernel's
-    mean launch time (K back-to-back first-pass launches between events);
+    payload + fp16 scales: 2*H*L*(D*b/8 + 2*D/G)) over the fused decode
+    kernel's mean launch time (the K back-to-back steps between events: one
+    launch per step); the split pass alone (va_decode_splits, K back-to-back
+    launches) is reported beside it;
   * cpu_baseline: the oracle's double-precision reference attention
     (reference(), src/voltattn.cu:769-794) over the same shape, timed on this
     host (rank 0, N=1 only).
@@ -172,6 +174,114 @@ def time_workload(va, w: Workload, steps: int, warmup: int, stream) -> dict:
     return {"mean_ms": mean_ms, "best_ms": best_ms, "kernel_ms": kern_ms}
 
 
+def time_fn(va, fn, copies: int, steps: int, warmup: int, stream) -> float:
+    """Mean ms of `steps` back-to-back calls fn(copy, stream), rotating copies."""
+    e0, e1 = va.Event(), va.Event()
+    try:
+        for c in range(copies):
+            fn(c, stream)
+        for i in range(warmup):
+            fn(i % copies, stream)
+        va.sync()
+        e0.record(stream)
+        for i in range(steps):
+            fn(i % copies, stream)
+        e1.record(stream)
+        e1.synchronize()
+        va.sync()
+        return e0.elapsed_ms(e1) / steps
+    finally:
+        e0.destroy()
+        e1.destroy()
+
+
+def bench_gqa(va, fmt, Hq, Hkv, L, D, G, steps, warmup, stream, min_set) -> dict:
+    """Grouped-query decode of one sequence (va_decode_gqa) over rotated KV copies."""
+    w = Workload(va, fmt, Hkv, L, D, G, min_set, 256)
+    try:
+        S = va.pick_splits_gqa(fmt, Hq, Hkv, L, D)
+        w.set_splits(S)
+        q = w._alloc(Hq * D * 2)
+        out = w._alloc(Hq * D * 2)
+        ws = w._alloc(va.ws_bytes(Hq, D, S))
+        x = w._alloc(Hq * D * 4)
+        va.fill_normal(x.ptr, Hq * D, 0x9999)
+        va.f32_to_f16(x.ptr, Hq * D, q.ptr)
+        va.sync()
+        bl = []
+        for c in range(w.copies):
+            b = w.bufs_for(c)
+            b.q, b.out, b.ws = q.ptr, out.ptr, ws.ptr
+            bl.append(b)
+        ms = time_fn(va, lambda c, st: va.decode_gqa(fmt, bl[c], Hq, Hkv, L, D, S=S, G=G, stream=st),
+                     w.copies, steps, warmup, stream)
+        return {"ms": ms, "S": S, "copies": w.copies, "bytes": w.copy_bytes}
+    finally:
+        w.free()
+
+
+def bench_paged(va, fmt, B, Hq, Hkv, L, P, D, G, steps, warmup, stream, min_set) -> dict:
+    """Paged batch decode (va_decode_paged): B sequences of L positions in pages of
+    P rows, pages of a sequence scattered over the pool by a shuffled block table."""
+    import numpy as np
+    npg = L // P
+    num_pages = B * npg
+    pay = va.page_bytes(fmt, Hkv, P, D) * num_pages
+    sc = va.page_scale_bytes(fmt, Hkv, P, D, G) * num_pages
+    per = 2 * (pay + sc)
+    copies = max(1, min(256, math.ceil(min_set / per)))
+    al = lambda x: (x + 4095) // 4096 * 4096
+    pa, sa = al(pay), al(max(sc, 1))
+    bufs = []
+    def alloc(n):
+        bufs.append(va.DeviceBuffer(n))
+        return bufs[-1]
+    try:
+        k, v = alloc(pa * copies), alloc(pa * copies)
+        sk = sv = None
+        if sc:
+            sk, sv = alloc(sa * copies), alloc(sa * copies)
+        # copy 0: quantize N(0,1) rows page by page (the layout is the pool's; values only
+        # need to be finite), then replicate
+        rows = num_pages * Hkv * P
+        x = alloc(rows * D * 4)
+        bits = va.fmt_bits(fmt)
+        for dst, sdst, s in ((k, sk, 11), (v, sv, 12)):
+            va.fill_normal(x.ptr, rows * D, s)
+            if bits == 16:
+                va.f32_to_f16(x.ptr, rows * D, dst.ptr)
+            else:
+                va.quantize(bits, G, x.ptr, rows, D, dst.ptr, sdst.ptr)
+        va.sync()
+        for c in range(1, copies):
+            for t in (k, v):
+                va.check(va.lib.va_memcpy_d2d(t.ptr + c * pa, t.ptr, pay, None))
+            if sc:
+                for t in (sk, sv):
+                    va.check(va.lib.va_memcpy_d2d(t.ptr + c * sa, t.ptr, sc, None))
+        table = np.random.default_rng(5).permutation(num_pages).astype(np.int32).reshape(B, npg)
+        tab = alloc(table.nbytes)
+        tab.upload(table)
+        lens = alloc(B * 4)
+        lens.upload(np.full(B, L, np.int32))
+        q, out = alloc(B * Hq * D * 2), alloc(B * Hq * D * 2)
+        va.fill_normal(x.ptr, B * Hq * D, 0x7777)
+        va.f32_to_f16(x.ptr, B * Hq * D, q.ptr)
+        shape = va.PagedShape(B, Hq, Hkv, D, G, P, npg, num_pages, L)
+        S = va.pick_splits_paged(fmt, shape)
+        ws = alloc(va.ws_bytes(B * Hq, D, S))
+        va.sync()
+        bl = [va.PagedBufs(K=k.ptr + c * pa, V=v.ptr + c * pa, scK=sk.ptr + c * sa if sk else 0,
+                           scV=sv.ptr + c * sa if sv else 0, block_table=tab.ptr, seq_lens=lens.ptr,
+                           q=q.ptr, out=out.ptr, ws=ws.ptr) for c in range(copies)]
+        ms = time_fn(va, lambda c, st: va.decode_paged(fmt, bl[c], shape, S, stream=st),
+                     copies, steps, warmup, stream)
+        return {"ms": ms, "S": S, "copies": copies, "bytes": per}
+    finally:
+        for b in bufs:
+            b.free()
+
+
 def cpu_baseline(H, L, D, G) -> dict:
     """The oracle's reference() on one full decode step of the workload (q8 inputs)."""
     import numpy as np
@@ -230,6 +340,8 @@ def main() -> int:
     ap.add_argument("--probe-gib", type=float, default=4.0)
     ap.add_argument("--set-gib", type=float, default=2.0, help="rotated working set per format")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-extra", action="store_true",
+                    help="skip the grouped-query and paged workloads (reported under 'extra')")
     ap.add_argument("--copy-probe-mib", type=int, default=0,
                     help="first run one plain device-to-device copy of this many MiB "
                          "(calibrates rocprof FETCH_SIZE/WRITE_SIZE against known bytes)")
@@ -289,6 +401,31 @@ def main() -> int:
             f"mean {r['ms'] * 1e3:8.2f} us  best {r['best_single_ms'] * 1e3:8.2f} us  "
             f"kernel {r['kernel_ms'] * 1e3:8.2f} us  {gbs:7.1f} GB/s  MBU {100 * r['mbu']:5.1f}%  "
             f"tok/s {r['tok_s']:8.0f}")
+    extra = {}
+    if not args.no_extra:
+        # Beyond the reference (grouped-query attention, paged batches): same bytes
+        # definition (K+V payload + scales actually read), tok/s per decode step.
+        min_set = int(args.set_gib * 2**30)
+        specs = [("gqa", "q8+", dict(Hq=32, Hkv=8, L=65536)), ("gqa", "f16+", dict(Hq=32, Hkv=8, L=65536)),
+                 ("gqa", "q4+", dict(Hq=32, Hkv=8, L=65536)),
+                 ("paged", "q8+", dict(B=8, Hq=32, Hkv=8, L=16384, P=256)),
+                 ("paged", "q8+", dict(B=1, Hq=32, Hkv=32, L=16384, P=256))]
+        for kind, name, p in specs:
+            fmt = va.Fmt.parse(name)
+            if kind == "gqa":
+                r = bench_gqa(va, fmt, p["Hq"], p["Hkv"], p["L"], D, G, args.steps, args.warmup, stream, min_set)
+                key = f"gqa {name} Hq={p['Hq']} Hkv={p['Hkv']} L={p['L']}"
+                seqs = 1
+            else:
+                r = bench_paged(va, fmt, p["B"], p["Hq"], p["Hkv"], p["L"], p["P"], D, G, args.steps,
+                                args.warmup, stream, min_set)
+                key = f"paged {name} B={p['B']} Hq={p['Hq']} Hkv={p['Hkv']} L={p['L']} page={p['P']}"
+                seqs = p["B"]
+            gbs = r["bytes"] / (r["ms"] * 1e6)
+            extra[key] = {"ms": r["ms"], "tok_s": seqs * 1e3 / r["ms"], "gbps": gbs, "mbu": gbs / ceiling,
+                          "bytes": r["bytes"], "S": r["S"], "copies": r["copies"]}
+            log(f"{key:48s} S={r['S']:3d}  mean {r['ms'] * 1e3:8.2f} us  {gbs:7.1f} GB/s  "
+                f"MBU {100 * gbs / ceiling:5.1f}%  tok/s {seqs * 1e3 / r['ms']:8.0f}")
     stream.destroy()
     for r in rows.values():
         if "f16" in rows:
@@ -297,12 +434,16 @@ def main() -> int:
             r["vs_f16p"] = rows["f16+"]["ms"] / r["ms"]
 
     head = rows[args.headline]
-    kern_gbs = head["kernel_gbps"]
-    roofline = {"bound": "hbm", "achieved": kern_gbs, "peak": PEAK_HBM_GBPS, "unit": "GB/s",
-                "frac": kern_gbs / PEAK_HBM_GBPS, "traffic": load_traffic(f"{args.headline}_L{L}_G{G}"),
-                "kernel": f"decode_tiled<{args.headline}> (first pass)",
+    # The step is one launch of the fused kernel (split-L pass + last-group LSE
+    # merge), so its mean back-to-back duration over the timed region is the
+    # kernel's launch duration; the split pass alone is reported beside it.
+    step_gbs = head["gbps"]
+    roofline = {"bound": "hbm", "achieved": step_gbs, "peak": PEAK_HBM_GBPS, "unit": "GB/s",
+                "frac": step_gbs / PEAK_HBM_GBPS, "traffic": load_traffic(f"{args.headline}_L{L}_G{G}"),
+                "kernel": f"decode_tiled<{args.headline}> fused (split-L pass + LSE merge, one launch per step)",
                 "algorithmic_bytes_per_launch": head["bytes"],
-                "kernel_ms": head["kernel_ms"], "frac_of_probed": kern_gbs / ceiling}
+                "kernel_ms": head["ms"], "frac_of_probed": step_gbs / ceiling,
+                "split_pass_only_ms": head["kernel_ms"], "split_pass_only_gbps": head["kernel_gbps"]}
     cpu = None
     if not args.no_cpu:
         cpu = cpu_baseline(H, L, D, G)
@@ -325,6 +466,7 @@ def main() -> int:
         "probed_ceiling_gbps": ceiling,
         "mbu": head["mbu"],
         "formats": rows,
+        "extra": extra,
         "device": info["name"], "compute_units": info["compute_units"],
     }
     print(json.dumps(line), flush=True)
