@@ -60,14 +60,19 @@ def test_paged_split_counts(fmt, S):
         _check(got[b].ravel(), pb.ref[b].ravel(), (fmt.label, S, b))
 
 
-def test_paged_d64_g64():
-    pb = batch_util.PagedBatch(va.Fmt.Q4M, [700, 129], 8, 2, 64, 64, 128, seed=9)
+@pytest.mark.parametrize("fmt", TILED, ids=lambda f: f.label)
+@pytest.mark.parametrize("page_rows", [64, 128])
+def test_paged_d64_g64(fmt, page_rows):
+    """D = 64 at the smallest page: q4 reads 32 rows per wave load, so its wave
+    tile must shrink to stay inside one 64-row page."""
+    print(f"paged d64 {fmt.label} P={page_rows}", flush=True)
+    pb = batch_util.PagedBatch(fmt, [700, 129, 64], 8, 2, 64, 64, page_rows, seed=9 + page_rows)
     try:
         got = pb.run()
     finally:
         pb.free()
-    for b in range(2):
-        _check(got[b].ravel(), pb.ref[b].ravel(), b)
+    for b in range(3):
+        _check(got[b].ravel(), pb.ref[b].ravel(), (fmt.label, b))
 
 
 def test_paged_many_sequences_two_pass():

@@ -3,41 +3,96 @@
 // GQA and paged KV as missing); the row format, quantization and arithmetic
 // are the reference path's.
 //
-// Every launch uses 4-wave work-groups. The query slots a work-group carries
-// (QG, the query heads that share one unpacked K/V row) are capped per kind by
-// the register budget of its o accumulators (QG x EPL fp32 per lane): f16 and
-// q8 up to 8, q4 up to 4, q3 up to 2; larger GQA groups run as several
-// sub-groups over the same rows. The tile depth U shrinks as QG grows so the
-// two register stages of K/V loads still fit.
+// The query slots a work-group carries (QG, the query heads that share one
+// unpacked K/V row) are capped per kind (max_query_slots); larger GQA groups
+// run as several sub-groups over the same rows, a group that is not a multiple
+// of QG masks the spare slots. Grouped work-groups are 8 waves (two per SIMD)
+// where that fits in 256 VGPRs, else 4; the tile depth U shrinks as QG grows
+// so the two register stages of K/V loads still fit.
 #include "va_tiled.hpp"
+
+#include <algorithm>
+#include <cstdlib>
 
 namespace va {
 
-constexpr int EX_WAVES = 4;
+// Launch shape of the grouped/paged kernels (VA_EX_MODE):
+//   0: 4-wave work-groups, one per CU;
+//   1: 4-wave work-groups, two per CU where two waves per SIMD fit in 256 VGPRs;
+//   2: 8-wave work-groups (two waves per SIMD from one group) where they fit,
+//      else as 0.
+// Two waves per SIMD hide the latency of the longer per-row chains of several
+// query heads; one wider group keeps the split count (and so the merge) as in 0.
+#ifndef VA_EX_MODE
+#define VA_EX_MODE 2
+#endif
 
+// Query slots per work-group, per kind: the largest QG whose 8-wave form (two
+// waves per SIMD) fits in 256 VGPRs. Measured on MI355X (Hq/Hkv = 32/8, 64/8,
+// 28/4 at L = 16K-64K): QG = 4 at two waves per SIMD beats QG = 8 at one for
+// f16 and q8 (groups of 8 run as two sub-groups, 12-38% faster), and q4 is
+// fastest at QG = 2 (QG = 4 spills at two waves per SIMD). VA_EX_QMAX=1|2|4
+// lowers the cap (a tuning switch, read once).
 int max_query_slots(int kind) {
-    switch (kind) {
-        case KF16: return 8;
-        case KQ8:  return 8;
-        case KQ4:  return 4;
-        default:   return 2;
+    static const int cap = [] { const char* e = std::getenv("VA_EX_QMAX"); return e ? std::atoi(e) : 0; }();
+    const int q = (kind == KF16 || kind == KQ8) ? 4 : 2;
+    return (cap == 1 || cap == 2 || cap == 4) ? std::min(q, cap) : q;
+}
+
+// Rows per lane per tile (U), waves per work-group and work-groups per CU
+// (MINB) for (kind, QG). FIT: two waves per SIMD fit in 256 VGPRs without
+// spilling at the shallower depth U2 (measured with the compiler's register
+// report), and the 8-wave LDS reduction fits (QG <= 4).
+template <int KIND, int QG> struct ExBase;
+template <int QG> struct ExBase<KF16, QG> { static constexpr int U = QG <= 2 ? 8 : 4, U2 = QG <= 2 ? 8 : 4; static constexpr bool FIT = QG == 2 || QG == 4; };
+template <int QG> struct ExBase<KQ8, QG>  { static constexpr int U = QG <= 4 ? 4 : 2, U2 = QG <= 2 ? 4 : 2; static constexpr bool FIT = QG == 2 || QG == 4; };
+template <int QG> struct ExBase<KQ4, QG>  { static constexpr int U = QG <= 2 ? 4 : 2, U2 = 2; static constexpr bool FIT = QG == 2; };
+template <int QG> struct ExBase<KQ3, QG>  { static constexpr int U = 2, U2 = 1; static constexpr bool FIT = QG == 2; };
+
+template <int KIND, int QG> struct ExCfg {
+    using B = ExBase<KIND, QG>;
+    static constexpr bool two = B::FIT && VA_EX_MODE != 0;
+    static constexpr int U     = two ? B::U2 : B::U;
+    static constexpr int WAVES = two && VA_EX_MODE == 2 ? 8 : 4;
+    static constexpr int MINB  = two && VA_EX_MODE == 1 ? 2 : 1;
+};
+
+template <int KIND>
+static int minb_of(int qg) {
+    switch (qg) {
+        case 1: return ExCfg<KIND, 1>::MINB;
+        case 2: return ExCfg<KIND, 2>::MINB;
+        default: return ExCfg<KIND, 4>::MINB;
     }
 }
 
-// Rows per lane per tile (U) for (kind, QG).
-template <int KIND, int QG> struct ExDepth;
-template <int QG> struct ExDepth<KF16, QG> { static constexpr int U = QG <= 2 ? 8 : 4; };
-template <int QG> struct ExDepth<KQ8, QG>  { static constexpr int U = QG <= 4 ? 4 : 2; };
-template <int QG> struct ExDepth<KQ4, QG>  { static constexpr int U = QG <= 2 ? 4 : 2; };
-template <int QG> struct ExDepth<KQ3, QG>  { static constexpr int U = 2; };
+int ex_groups_per_cu(int kind, int qg) {
+    switch (kind) {
+        case KF16: return minb_of<KF16>(qg);
+        case KQ8:  return minb_of<KQ8>(qg);
+        case KQ4:  return minb_of<KQ4>(qg);
+        default:   return minb_of<KQ3>(qg);
+    }
+}
 
-// The largest work-group tile over the QG variants of a kind: split lengths
-// are multiples of it, so every variant starts its splits on a tile boundary.
+// Rows per lane actually used: a wave tile (PPW * U rows) must fit in the
+// smallest page (64 rows), e.g. q4 at D = 64 reads 32 rows per wave load.
+template <int KIND, int D, int QG>
+constexpr int ex_unroll() {
+    return ExCfg<KIND, QG>::U < 64 / Tile<KIND, D>::PPW ? ExCfg<KIND, QG>::U : 64 / Tile<KIND, D>::PPW;
+}
+
+template <int KIND, int D, int QG>
+constexpr int ex_tile() {
+    return Tile<KIND, D>::PPW * ex_unroll<KIND, D, QG>() * ExCfg<KIND, QG>::WAVES;
+}
+
+// The largest work-group tile over the QG variants of a kind (all are powers
+// of two): split lengths are multiples of it, so every variant starts its
+// splits on a tile boundary.
 template <int KIND, int D>
 static int max_tile() {
-    constexpr int PPW = Tile<KIND, D>::PPW;
-    constexpr int u = ExDepth<KIND, 1>::U;
-    return PPW * u * EX_WAVES;
+    return std::max(std::max(ex_tile<KIND, D, 1>(), ex_tile<KIND, D, 2>()), ex_tile<KIND, D, 4>());
 }
 
 int tile_positions_ex(int kind, int D) {
@@ -51,9 +106,11 @@ int tile_positions_ex(int kind, int D) {
 
 template <int KIND, int D, int G, int QG, bool PAGED>
 static hipError_t launch_ex(int groups, const DecodeArgs& a, hipStream_t st) {
-    constexpr int U = ExDepth<KIND, QG>::U;
-    hipLaunchKernelGGL((decode_tiled<KIND, D, G, U, EX_WAVES, QG, PAGED>),
-                       dim3((unsigned)(groups * a.S)), dim3(EX_WAVES * 64), 0, st, a);
+    using Cfg = ExCfg<KIND, QG>;
+    constexpr int U = ex_unroll<KIND, D, QG>();
+    static_assert(Tile<KIND, D>::PPW * U <= 64, "a wave tile must fit the smallest page");
+    hipLaunchKernelGGL((decode_tiled<KIND, D, G, U, Cfg::WAVES, QG, PAGED, Cfg::MINB>),
+                       dim3((unsigned)(groups * a.S)), dim3(Cfg::WAVES * 64), 0, st, a);
     return hipGetLastError();
 }
 
@@ -65,12 +122,9 @@ static hipError_t launch_qg(int qg, int groups, const DecodeArgs& a, hipStream_t
             else return hipErrorInvalidValue;       // QG = 1 contiguous: va_decode.hip
         case 2: return launch_ex<KIND, D, G, 2, PAGED>(groups, a, st);
         case 4:
-            if constexpr (KIND != KQ3) return launch_ex<KIND, D, G, 4, PAGED>(groups, a, st);
+            if constexpr (KIND == KF16 || KIND == KQ8) return launch_ex<KIND, D, G, 4, PAGED>(groups, a, st);
             else return hipErrorInvalidValue;
-        case 8:
-            if constexpr (KIND == KF16 || KIND == KQ8) return launch_ex<KIND, D, G, 8, PAGED>(groups, a, st);
-            else return hipErrorInvalidValue;
-        default: return hipErrorInvalidValue;
+        default: return hipErrorInvalidValue;          // above max_query_slots(kind)
     }
 }
 

@@ -69,6 +69,8 @@ hipError_t launch_decode_ex(int kind, int D, int G, int qg, bool paged, int grou
 // work-group tile (positions per iteration) of the grouped/paged kernels.
 int max_query_slots(int kind);
 int tile_positions_ex(int kind, int D);
+// Work-groups per CU the grouped/paged launch of (kind, QG) is built for.
+int ex_groups_per_cu(int kind, int qg);
 
 // Work-groups per CU the split rule aims for (tiled kernels: the configured
 // groups per CU of the kind; naive kernels: 8).

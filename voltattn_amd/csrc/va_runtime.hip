@@ -220,11 +220,13 @@ void pick_qg(int kind, int qgroup, int* qg, int* nsub) {
 }
 
 // Split count and split length for `groups` merge groups over sequences of up
-// to max_len positions: one 4-wave work-group per CU, splits of whole kernel
-// tiles, at most 64 splits (the fused merge's limit). S_req > 0 fixes S.
-void splits_ex(int kind, int D, int groups, int max_len, int S_req, int* S, int* chunk) {
+// to max_len positions: the kernel's work-groups per CU (one or two 4-wave
+// groups), splits of whole kernel tiles, at most 64 splits (the fused merge's
+// limit). S_req > 0 fixes S.
+void splits_ex(int kind, int D, int qg, int groups, int max_len, int S_req, int* S, int* chunk) {
     int cus = cu_count();
     if (cus <= 0) cus = 256;
+    cus *= va::ex_groups_per_cu(kind, qg);
     const int tb = va::tile_positions_ex(kind, D);
     const int tiles = std::max(1, (max_len + tb - 1) / tb);
     int s0 = S_req;
@@ -265,7 +267,7 @@ int va_pick_splits_gqa(va_fmt fmt, int Hq, int Hkv, int L, int D, int* S) {
     if (!tiled_of(fmt)) return fail(VA_EINVAL, "grouped-query decode needs a tiled format (f16+, q8+, q4+, q3+)");
     int qg, nsub, chunk;
     pick_qg(kind_of(fmt), Hq / Hkv, &qg, &nsub);
-    splits_ex(kind_of(fmt), D, Hkv * nsub, L, 0, S, &chunk);
+    splits_ex(kind_of(fmt), D, qg, Hkv * nsub, L, 0, S, &chunk);
     return VA_OK;
 }
 
@@ -289,7 +291,7 @@ int va_decode_gqa(va_fmt fmt, const va_bufs* b, int Hq, int Hkv, int L, int D, i
     int qg, nsub, Sx, chunk;
     pick_qg(kind_of(fmt), Hq / Hkv, &qg, &nsub);
     const int groups = Hkv * nsub;
-    splits_ex(kind_of(fmt), D, groups, L, S, &Sx, &chunk);
+    splits_ex(kind_of(fmt), D, qg, groups, L, S, &Sx, &chunk);
     if ((long long)Hq * Sx > 0x7FFFFFFFLL || (long long)groups * Sx > 0x7FFFFFFFLL)
         return fail(VA_ERANGE, "Hq*S too large");
     va::DecodeArgs a{};
@@ -357,10 +359,10 @@ int va_pick_splits_paged(va_fmt fmt, const va_paged_shape* sh, int* S) {
     if (rc) return rc;
     int qg, nsub, chunk;
     pick_qg(kind_of(fmt), sh->Hq / sh->Hkv, &qg, &nsub);
-    splits_ex(kind_of(fmt), sh->D, sh->B * sh->Hkv * nsub, std::max(1, sh->max_seq_len), 0, S, &chunk);
+    splits_ex(kind_of(fmt), sh->D, qg, sh->B * sh->Hkv * nsub, std::max(1, sh->max_seq_len), 0, S, &chunk);
     // a split may span at most MAX_SPLIT_PAGES pages
     while ((chunk / sh->page_rows) + 2 > va::MAX_SPLIT_PAGES && *S < 0x7FFF) {
-        splits_ex(kind_of(fmt), sh->D, sh->B * sh->Hkv * nsub, std::max(1, sh->max_seq_len), *S * 2, S, &chunk);
+        splits_ex(kind_of(fmt), sh->D, qg, sh->B * sh->Hkv * nsub, std::max(1, sh->max_seq_len), *S * 2, S, &chunk);
     }
     return VA_OK;
 }
@@ -394,7 +396,7 @@ int va_decode_paged(va_fmt fmt, const va_paged_bufs* b, const va_paged_shape* sh
         if (rc) return rc;
         S = Sx;
     }
-    splits_ex(kind_of(fmt), sh->D, (int)std::min<long long>(groups, 1 << 30), std::max(1, sh->max_seq_len), S,
+    splits_ex(kind_of(fmt), sh->D, qg, (int)std::min<long long>(groups, 1 << 30), std::max(1, sh->max_seq_len), S,
               &Sx, &chunk);
     if (chunk / sh->page_rows + 2 > va::MAX_SPLIT_PAGES)
         return fail(VA_EINVAL, "a split of %d positions spans more than %d pages; raise S", chunk,

@@ -47,8 +47,8 @@ namespace va {
 constexpr float RESCALE_SLACK = 8.0f;    // log2 units: weights stay <= 256
 constexpr float M_INIT = -1e30f;         // finite "no score yet" maximum
 
-template <int KIND, int D, int G, int U, int WAVES, int QG, bool PAGED>
-__global__ __launch_bounds__(WAVES * 64) void decode_tiled(DecodeArgs a) {
+template <int KIND, int D, int G, int U, int WAVES, int QG, bool PAGED, int MINB = 1>
+__global__ __launch_bounds__(WAVES * 64, MINB) void decode_tiled(DecodeArgs a) {
     using T = Tile<KIND, D>;
     using C = Codec<KIND>;
     using LoadT = typename LaneLoad<KIND>::type;
