@@ -40,6 +40,9 @@ HIPCC_FLAGS = [
     "-Wno-unused-command-line-argument",
     # Keep hipcc from forming packed-FP32 (v_pk_*_f32) instructions.
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # MFMA accumulators in arch VGPRs (the matrix-core decode fits in 256 of
+    # them); the AGPR form shuttled them through v_accvgpr moves.
+    "-mllvm", "-amdgpu-mfma-vgpr-form=1",
 ]
 
 

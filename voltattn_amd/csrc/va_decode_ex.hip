@@ -10,6 +10,7 @@
 // where that fits in 256 VGPRs, else 4; the tile depth U shrinks as QG grows
 // so the two register stages of K/V loads still fit.
 #include "va_tiled.hpp"
+#include "va_mfma.hpp"
 
 #include <algorithm>
 #include <cstdlib>
@@ -26,6 +27,22 @@ namespace va {
 #ifndef VA_EX_MODE
 #define VA_EX_MODE 2
 #endif
+
+// Matrix-core form (va_mfma.hpp) for q8 rows with two or more query slots:
+// MFMA_WAVES waves per work-group, 32-row wave tiles. VA_MFMA=0 in the
+// environment selects the VALU form instead (a tuning switch, read once).
+#ifndef VA_MFMA_WAVES
+#define VA_MFMA_WAVES 8
+#endif
+constexpr int MFMA_WAVES = VA_MFMA_WAVES;
+constexpr int MFMA_TILE  = 32 * MFMA_WAVES;
+
+static bool mfma_on() {
+    static const bool on = [] { const char* e = std::getenv("VA_MFMA"); return !(e && e[0] == '0'); }();
+    return on;
+}
+
+static bool mfma_form(int kind, int qg) { return kind == KQ8 && qg >= 2 && mfma_on(); }
 
 // Query slots per work-group, per kind: the largest QG whose 8-wave form (two
 // waves per SIMD) fits in 256 VGPRs. Measured on MI355X (Hq/Hkv = 32/8, 64/8,
@@ -67,6 +84,7 @@ static int minb_of(int qg) {
 }
 
 int ex_groups_per_cu(int kind, int qg) {
+    if (mfma_form(kind, qg)) return 1;
     switch (kind) {
         case KF16: return minb_of<KF16>(qg);
         case KQ8:  return minb_of<KQ8>(qg);
@@ -98,7 +116,7 @@ static int max_tile() {
 int tile_positions_ex(int kind, int D) {
     switch (kind) {
         case KF16: return D == 128 ? max_tile<KF16, 128>() : max_tile<KF16, 64>();
-        case KQ8:  return D == 128 ? max_tile<KQ8, 128>()  : max_tile<KQ8, 64>();
+        case KQ8:  return std::max(MFMA_TILE, D == 128 ? max_tile<KQ8, 128>() : max_tile<KQ8, 64>());
         case KQ4:  return D == 128 ? max_tile<KQ4, 128>()  : max_tile<KQ4, 64>();
         default:   return D == 128 ? max_tile<KQ3, 128>()  : max_tile<KQ3, 64>();
     }
@@ -106,6 +124,13 @@ int tile_positions_ex(int kind, int D) {
 
 template <int KIND, int D, int G, int QG, bool PAGED>
 static hipError_t launch_ex(int groups, const DecodeArgs& a, hipStream_t st) {
+    if constexpr (KIND == KQ8 && QG >= 2) {
+        if (mfma_on()) {
+            hipLaunchKernelGGL((decode_mfma<KIND, D, G, MFMA_WAVES, QG, PAGED>),
+                               dim3((unsigned)(groups * a.S)), dim3(MFMA_WAVES * 64), 0, st, a);
+            return hipGetLastError();
+        }
+    }
     using Cfg = ExCfg<KIND, QG>;
     constexpr int U = ex_unroll<KIND, D, QG>();
     static_assert(Tile<KIND, D>::PPW * U <= 64, "a wave tile must fit the smallest page");

@@ -1,0 +1,403 @@
+// va_mfma.hpp — grouped-query decode on the matrix cores (gfx950 MFMA).
+//
+// Same partials as decode_tiled (va_tiled.hpp), for the q8 rows, with q.K and
+// P.V as v_mfma_f32_16x16x32_f16 products instead of per-lane dot/axpy chains
+// (the VALU form spends ~28 vector instructions per position at four query
+// heads; here the matrix core does the multiply-adds and the VALU keeps the
+// unpack, the softmax and the operand set-up).
+//
+// MFMA 16x16x32 f16 lane layout (probed on MI355X): lane l holds
+// A[l%16][8(l/16)+e] and B[8(l/16)+e][l%16] (e = 0..7) and receives
+// D[4(l/16)+v][l%16] (v = 0..3). Below, quarter g = l/16 and column n = l%16.
+//
+// q.K — one 16-row block of positions per MFMA row index, k = dimensions.
+//   A = K codes of 16 rows: lane (g, n) loads the D/4 contiguous bytes
+//       [g*D/4, (g+1)*D/4) of row n and turns them into exact fp16 integers.
+//   B = q^T with the scale groups stacked as columns: column n = cg*QP + cq
+//       (QP = 16/NG column slots per group) holds query slot cq restricted to
+//       the dimensions of scale group cg (zero elsewhere). Every product
+//       code*q is exact in fp32, so each output column is the exact partial
+//       dot of one (query, group); the per-position group scales are applied
+//       afterwards in fp32 and the NG columns of a query are summed with DPP
+//       row rotations (every replica gets the same bits).
+// P.V — k = positions, 32 per MFMA (the two q.K blocks).
+//   A = P * s_v with the same stacked rows: row n = (cg, cq) carries
+//       p[cq][pos] * s_v[pos][cg]. Lane (g, n) already holds the scores of
+//       exactly the positions of its k slots (16c + 4g + v), so no data moves.
+//       The fp32 value is split into fp16 hi + lo (RNE), two MFMAs, so P.V
+//       keeps ~22 significant bits (MFMA keeps fp16 subnormals; probed).
+//   B = V codes transposed: the wave's V tile is staged in LDS row-major and
+//       read with ds_read_b64_tr_b8 (within 16 lanes, lane i receives byte i of
+//       each 16-byte row formed by the chunks of lanes 2e and 2e+1), giving each
+//       lane 8 positions of one column.
+//   Output row (cg, cq), column d is useful when d lies in scale group cg;
+//   each (query, dimension) is produced by exactly one lane and accumulator.
+// Softmax: log2 units (q pre-scaled by log2(e)/sqrt(D) in fp32 after the dot),
+// lazy running maximum per query slot as in decode_tiled (RESCALE_SLACK).
+//
+// Work split, loads and the merge are decode_tiled's: one work-group per
+// (merge group, split), per-wave 32-row tiles double-buffered in registers,
+// buffer resources bounded by the split (or per tile for paged caches), and
+// finish_partial for the partials / fused merge.
+#pragma once
+#include "va_codec.hpp"
+#include "va_fused.hpp"
+#include "va_tiled.hpp"
+
+namespace va {
+
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef int i32x2 __attribute__((ext_vector_type(2)));
+typedef __attribute__((address_space(3))) i32x2 lds_i32x2;
+
+__device__ __forceinline__ f32x4 mfma_16x16x32(const f16x8& a, const f16x8& b, const f32x4& c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+
+// 8 int8 codes (two dwords, byte order) -> 8 exact fp16 values in the same order.
+__device__ __forceinline__ f16x8 q8_to_f16x8(uint32_t w0, uint32_t w1, uint32_t magic) {
+    const uint32_t u0 = w0 ^ 0x80808080u, u1 = w1 ^ 0x80808080u;
+    const h2 bias = hh(1152.f, 1152.f);
+    const h2 p0 = as_h2(__builtin_amdgcn_perm(magic, u0, 0x04010400u)) - bias;
+    const h2 p1 = as_h2(__builtin_amdgcn_perm(magic, u0, 0x04030402u)) - bias;
+    const h2 p2 = as_h2(__builtin_amdgcn_perm(magic, u1, 0x04010400u)) - bias;
+    const h2 p3 = as_h2(__builtin_amdgcn_perm(magic, u1, 0x04030402u)) - bias;
+    return f16x8{p0.x, p0.y, p1.x, p1.y, p2.x, p2.y, p3.x, p3.y};
+}
+
+template <int KIND, int D, int G, int WAVES, int QG, bool PAGED>
+__global__ __launch_bounds__(WAVES * 64, 1) void decode_mfma(DecodeArgs a) {
+    static_assert(KIND == KQ8, "matrix-core form: q8 rows");
+    constexpr int ROWB = D;                      // q8: one byte per element
+    constexpr int NG   = D / G;                  // scale groups per row (1, 2, 4)
+    constexpr int QP   = 16 / NG;                // column slots per scale group
+    static_assert(QG >= 1 && QG <= QP, "query slots per work-group");
+    constexpr int TW   = 32;                     // rows per wave tile (two 16-row blocks)
+    constexpr int TB   = TW * WAVES;
+    constexpr int DQ   = D / 4;                  // row bytes per lane quarter (A operand)
+    constexpr int KL   = DQ / 16;                // 16-byte K loads per block per lane
+    constexpr int NJ   = D / 32;                 // q.K MFMAs per block
+    constexpr int NB   = D / 16;                 // P.V column blocks
+    constexpr int VL   = TW * ROWB / (64 * 16);  // 16-byte V loads per lane per tile
+    constexpr int VSTR = ROWB + 16;              // LDS row stride of the staged V tile
+    constexpr int VROWS = TW + 4;                // rows 16..31 sit 4 slots further
+    constexpr int SCE  = NG >= 2 ? TW * NG / 2 : TW;   // scale words (dwords, or halves at NG = 1)
+    static_assert(KL >= 1 && VL >= 1 && SCE <= 64, "tile shape");
+
+    __shared__ __align__(16) uint8_t  s_v[WAVES][VROWS * VSTR];
+    __shared__ __align__(16) uint32_t s_sc[WAVES][NG][TW];   // (k | v << 16) scale pairs
+    __shared__ float s_red[QG][WAVES][D];
+    __shared__ float s_l[QG][WAVES];
+    __shared__ float s_m[QG][WAVES];
+    __shared__ int   s_page[PAGED ? MAX_SPLIT_PAGES : 1];
+
+    // ---- work-group -> (sequence b, KV head hk, query sub-group, split s)
+    Route rt;
+    rt.mg = (int)blockIdx.x / a.S;
+    rt.s  = (int)blockIdx.x - rt.mg * a.S;
+    const int sub = rt.mg % a.nsub;
+    const int hk  = (rt.mg / a.nsub) % a.hkv;
+    const int b   = (rt.mg / a.nsub) / a.hkv;
+    rt.nq  = min(QG, a.qgroup - sub * QG);
+    rt.oh0 = (b * a.hkv + hk) * a.qgroup + sub * QG;
+    const int s = rt.s;
+    const unsigned epoch = read_epoch(a, rt.mg);
+    const int wave = uniform((int)(threadIdx.x >> 6));
+    const int lane = (int)(threadIdx.x & 63);
+    const int g    = lane >> 4;                  // quarter
+    const int col  = lane & 15;                  // column / row-in-block
+    const int cg   = col / QP;                   // scale group of this column
+    const int cq   = col % QP;                   // query slot of this column
+
+    int L = a.L;
+    bool bad = false;
+    if constexpr (PAGED) {
+        const int cap = min(a.L, min(a.S * a.chunk, a.max_pages << a.page_shift));
+        L = a.seq_lens[b];
+        if (L > cap) { bad = true; L = cap; }
+        L = max(L, 0);
+    }
+    const int j0 = s * a.chunk;
+    const int n  = min(L - j0, a.chunk);
+
+    // Per lane, for its column (cg, cq): running max mq and weight sum lsum of
+    // query slot cq, and the row exponent ex (the P.V operands and the o row of
+    // this column carry an exact factor 2^ex, |ex| <= 100).
+    float mq = M_INIT, ex = 0.f, lsum = 0.f;
+    f32x4 o[NB];
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) o[nb] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    if (n > 0) {
+        const int niter = (n + TB - 1) / TB;
+        const size_t   row0  = PAGED ? 0 : (size_t)hk * a.L + j0;
+        const uint32_t nsplt = PAGED ? 0u : (uint32_t)n;
+        const __amdgpu_buffer_rsrc_t rk  = make_rsrc(a.k + row0 * ROWB, nsplt * ROWB);
+        const __amdgpu_buffer_rsrc_t rv  = make_rsrc(a.v + row0 * ROWB, nsplt * ROWB);
+        const __amdgpu_buffer_rsrc_t rsk = make_rsrc(a.sk + row0 * NG, nsplt * NG * 2);
+        const __amdgpu_buffer_rsrc_t rsv = make_rsrc(a.sv + row0 * NG, nsplt * NG * 2);
+        int p0 = 0;
+        if constexpr (PAGED) {
+            p0 = j0 >> a.page_shift;
+            const int np = ((j0 + n - 1) >> a.page_shift) - p0 + 1;
+            const int32_t* tab = a.block_table + (size_t)b * a.max_pages + p0;
+            for (int i = (int)threadIdx.x; i < np; i += WAVES * 64) s_page[i] = tab[i];
+            __syncthreads();
+        }
+
+        const uint32_t koff = (uint32_t)(col * ROWB + g * DQ);     // K: row n, quarter g
+        const uint32_t soff_l = (uint32_t)min(lane, SCE - 1) * (NG >= 2 ? 4u : 2u);
+
+        u32x4 ka[2][KL], kb[2][KL], va_[VL], vb[VL];
+        uint32_t ska, sva, skb, svb;
+
+        auto load_tile = [&](int it, u32x4 (&kk)[2][KL], u32x4* vv, uint32_t& sk, uint32_t& sv) {
+            const int t0 = it * TB + wave * TW;
+            __amdgpu_buffer_rsrc_t tk = rk, tv = rv, tsk = rsk, tsv = rsv;
+            uint32_t soff = (uint32_t)t0;
+            if constexpr (PAGED) {
+                const int pos  = j0 + t0;
+                const int rows = max(0, min(TW, n - t0));
+                int page = 0;
+                if (rows > 0) page = uniform(s_page[(pos >> a.page_shift) - p0]);
+                const bool ok = page >= 0 && page < a.num_pages;
+                bad = bad || (rows > 0 && !ok);
+                const uint32_t nrow = ok ? (uint32_t)rows : 0u;
+                const size_t row = ((size_t)(ok ? page : 0) * a.hkv + hk) * ((size_t)1 << a.page_shift) +
+                                   (size_t)(pos & ((1 << a.page_shift) - 1));
+                tk  = make_rsrc(a.k + row * ROWB, nrow * ROWB);
+                tv  = make_rsrc(a.v + row * ROWB, nrow * ROWB);
+                tsk = make_rsrc(a.sk + row * NG, nrow * NG * 2);
+                tsv = make_rsrc(a.sv + row * NG, nrow * NG * 2);
+                soff = 0;
+            }
+            const uint32_t tpos = sgpr(soff);
+            __builtin_amdgcn_sched_barrier(0);
+            if constexpr (NG >= 2) {
+                sk = ld32(tsk, soff_l, tpos * NG * 2);
+                sv = ld32(tsv, soff_l, tpos * NG * 2);
+            } else {
+                sk = ld16(tsk, soff_l, tpos * 2);
+                sv = ld16(tsv, soff_l, tpos * 2);
+            }
+#pragma unroll
+            for (int c = 0; c < 2; ++c)
+#pragma unroll
+                for (int i = 0; i < KL; ++i)
+                    kk[c][i] = ld128(tk, koff + (uint32_t)(c * 16 * ROWB + 16 * i), tpos * ROWB);
+#pragma unroll
+            for (int i = 0; i < VL; ++i)
+                vv[i] = ld128(tv, (uint32_t)(16 * (64 * i + lane)), tpos * ROWB);
+            __builtin_amdgcn_sched_barrier(0);
+        };
+
+        load_tile(0, ka, va_, ska, sva);
+
+        // q^T operand of the q.K products: column (cg, cq), k slots of quarter g
+        // are dimensions g*DQ + 8j + e. Zero outside group cg and for unused slots.
+        f16x8 qb[NJ];
+        {
+            const bool live = cq < rt.nq;
+            const _Float16* qrow = reinterpret_cast<const _Float16*>(a.q) + (size_t)(rt.oh0 + (live ? cq : 0)) * D;
+#pragma unroll
+            for (int j = 0; j < NJ; ++j) {
+                const int d0 = g * DQ + 8 * j;
+                const bool use = live && (d0 / G) == cg;
+                const u32x4 w = *reinterpret_cast<const u32x4*>(qrow + d0);
+                const u32x4 z = use ? w : u32x4{0u, 0u, 0u, 0u};
+                qb[j] = __builtin_bit_cast(f16x8, z);
+            }
+        }
+        const uint32_t magic = [] { uint32_t m; VA_VGPR_CONST(m, 0x64646464); return m; }();
+        const float qs = a.qscale;
+
+        // tr8 source row of this lane: tr row e = col/2 is position 16(e/4) + 4g + e%4,
+        // half (col & 1) of a 16-byte column chunk.
+        const int te   = col >> 1;
+        const int tpos_row = 16 * (te >> 2) + 4 * g + (te & 3);
+        const uint32_t vrd = (uint32_t)((tpos_row + 4 * (te >> 2)) * VSTR + 8 * (col & 1));
+        uint8_t* const sv_w = &s_v[wave][0];
+
+        // Multiply accumulator rows by the per-column factor f of their column:
+        // accumulator row 4g + v is stacked row (column) 4g + v.
+        auto scale_rows = [&](f32x4 (&acc_o)[NB], float f) {
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                const float fv = __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute((4 * g + v) << 2, __builtin_bit_cast(int, f)));
+#pragma unroll
+                for (int nb = 0; nb < NB; ++nb) acc_o[nb][v] *= fv;
+            }
+        };
+
+        auto compute_tile = [&](int it, const u32x4 (&kk)[2][KL], const u32x4* vv, uint32_t sk, uint32_t sv) {
+            const int rem = uniform(n - (it * TB + wave * TW));
+            // V tile -> LDS (row-major, rows 16..31 shifted by 4 slots)
+#pragma unroll
+            for (int i = 0; i < VL; ++i) {
+                const int chunk = 64 * i + lane;
+                const int row = chunk / (ROWB / 16), c16 = chunk % (ROWB / 16);
+                *reinterpret_cast<u32x4*>(sv_w + (row + 4 * (row >> 4)) * VSTR + 16 * c16) = vv[i];
+            }
+            // scales -> LDS as (k | v << 16) pairs, [group][row]
+            if (lane < SCE) {
+                if constexpr (NG >= 2) {
+                    const int f = 2 * lane;
+                    s_sc[wave][f % NG][f / NG]             = __builtin_amdgcn_perm(sv, sk, 0x05040100u);
+                    s_sc[wave][(f + 1) % NG][(f + 1) / NG] = __builtin_amdgcn_perm(sv, sk, 0x07060302u);
+                } else {
+                    s_sc[wave][0][lane] = (sk & 0xFFFFu) | (sv << 16);
+                }
+            }
+            // q.K: two 16-row blocks, NJ MFMAs each
+            f32x4 acc[2];
+#pragma unroll
+            for (int c = 0; c < 2; ++c) acc[c] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int j = 0; j < NJ; ++j)
+#pragma unroll
+                for (int c = 0; c < 2; ++c) {
+                    const u32x4& w = kk[c][j / 2];
+                    const f16x8 kf = q8_to_f16x8(w[2 * (j % 2)], w[2 * (j % 2) + 1], magic);
+                    acc[c] = mfma_16x16x32(kf, qb[j], acc[c]);
+                }
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+            // scale pairs of this lane's 8 positions (16c + 4g + v), group cg
+            const u32x4 sc0 = *reinterpret_cast<const u32x4*>(&s_sc[wave][cg][4 * g]);
+            const u32x4 sc1 = *reinterpret_cast<const u32x4*>(&s_sc[wave][cg][16 + 4 * g]);
+            float x[8];
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                x[v]     = acc[0][v] * (h2f_lo(sc0[v]) * qs);
+                x[4 + v] = acc[1][v] * (h2f_lo(sc1[v]) * qs);
+            }
+            // sum the NG group columns of each query slot (row rotations by QP, 2QP)
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                if constexpr (NG == 4) { x[e] += dpp<dpp_row_ror(8)>(x[e]); x[e] += dpp<dpp_row_ror(4)>(x[e]); }
+                if constexpr (NG == 2) { x[e] += dpp<dpp_row_ror(8)>(x[e]); }
+            }
+            float tmax = -__builtin_inff();
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const int p = 16 * (e >> 2) + 4 * g + (e & 3);
+                if (p >= rem) x[e] = -__builtin_inff();
+                tmax = fmaxf(tmax, x[e]);
+            }
+            const bool raise = __builtin_amdgcn_ballot_w64(tmax > mq + RESCALE_SLACK) != 0;
+            if (raise) {
+                // new maximum of each query slot: over its NG columns and the 4 quarters
+                float mx = fmaxf(mq, tmax);
+                if constexpr (NG == 4) { mx = fmaxf(mx, dpp<dpp_row_ror(8)>(mx)); mx = fmaxf(mx, dpp<dpp_row_ror(4)>(mx)); }
+                if constexpr (NG == 2) { mx = fmaxf(mx, dpp<dpp_row_ror(8)>(mx)); }
+                mx = fmaxf(mx, swz_xor<16>(mx));
+                mx = fmaxf(mx, lane_xor32(mx));
+                const float c = fast_exp2(mq - mx);
+                mq = mx;
+                lsum *= c;
+                scale_rows(o, c);
+            }
+            // weights p and the operand values p * s_v * 2^ex (2^ex: exact scaling)
+            const float fe = __builtin_bit_cast(float, (uint32_t)(127 + (int)ex) << 23);
+            float xv[8], xmax = 0.f;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const float p = fast_exp2(x[e] - mq);
+                lsum += p;
+                const uint32_t pr = e < 4 ? sc0[e] : sc1[e - 4];
+                xv[e] = (p * h2f_hi(pr)) * fe;
+                xmax = fmaxf(xmax, xv[e]);
+            }
+            // Row exponent: keep operands <= 2^15 (fp16 range), and after a new
+            // maximum re-centre them near 2^14 so the lo halves stay normal.
+            if (raise || __builtin_amdgcn_ballot_w64(xmax > 32768.f)) {
+                float mc = fmaxf(xmax, swz_xor<16>(xmax));
+                mc = fmaxf(mc, lane_xor32(mc));                 // max of the row (column) over quarters
+                int dl = 0;
+                if (mc > 0.f) dl = 14 - ((int)((__builtin_bit_cast(uint32_t, mc) >> 23) & 0xFF) - 126);
+                dl = max(-100 - (int)ex, min(100 - (int)ex, dl));
+                const float f = __builtin_bit_cast(float, (uint32_t)(127 + dl) << 23);
+                ex += (float)dl;
+#pragma unroll
+                for (int e = 0; e < 8; ++e) xv[e] *= f;
+                scale_rows(o, f);
+            }
+            // fp16 hi + lo (both RNE), k slot e = 4c + v
+            f16x8 ahi, alo;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const _Float16 hi = (_Float16)xv[e];
+                ahi[e] = hi;
+                alo[e] = (_Float16)(xv[e] - (float)hi);
+            }
+            // P.V over NB column blocks: V^T operand from the staged tile
+#pragma unroll
+            for (int nb = 0; nb < NB; ++nb) {
+                const i32x2 t = __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_i32x2*)(sv_w + vrd + 16 * nb));
+                const f16x8 vf = q8_to_f16x8((uint32_t)t[0], (uint32_t)t[1], magic);
+                o[nb] = mfma_16x16x32(ahi, vf, o[nb]);
+                o[nb] = mfma_16x16x32(alo, vf, o[nb]);
+            }
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        };
+
+        const int npair = (niter + 1) / 2;
+        for (int ip = 0; ip < npair; ++ip) {
+            const int it = 2 * ip;
+            load_tile(it + 1, kb, vb, skb, svb);
+            compute_tile(it, ka, va_, ska, sva);
+            load_tile(it + 2, ka, va_, ska, sva);
+            compute_tile(it + 1, kb, vb, skb, svb);
+        }
+    }
+
+    // ---- work-group merge. Per query slot q: lsum of column q summed over the
+    // 4 quarters (every group column of q holds the same sum), m = mq; o row
+    // (cg', q) drops its row factor 2^ex (an exact power of two).
+    float lt = lsum + swz_xor<16>(lsum);
+    lt += lane_xor32(lt);
+    if (lane < QG) {
+        s_l[lane][wave] = lt;
+        s_m[lane][wave] = mq;
+    }
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+        const int r = 4 * g + v;                     // stacked row (r / QP, r % QP)
+        const float er = __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute(r << 2, __builtin_bit_cast(int, ex)));
+        const float f  = __builtin_bit_cast(float, (uint32_t)(127 - (int)er) << 23);
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb) {
+            const int d = 16 * nb + col;
+            if (r / QP == d / G && r % QP < QG) s_red[r % QP][wave][d] = o[nb][v] * f;
+        }
+    }
+    bool any_bad = false;
+    if constexpr (PAGED) any_bad = __syncthreads_or(bad);
+    else __syncthreads();
+    const int t = (int)threadIdx.x;
+    float M[QG], acc[QG], ls[QG];
+#pragma unroll
+    for (int q = 0; q < QG; ++q) {
+        M[q] = 0.f;
+        acc[q] = 0.f;
+        ls[q] = 0.f;
+        if (t < D) {
+            M[q] = s_m[q][0];
+#pragma unroll
+            for (int w = 1; w < WAVES; ++w) M[q] = fmaxf(M[q], s_m[q][w]);
+#pragma unroll
+            for (int w = 0; w < WAVES; ++w) {
+                const float f = fast_exp2(s_m[q][w] - M[q]);
+                acc[q] = __builtin_fmaf(f, s_red[q][w][t], acc[q]);
+                ls[q]  = __builtin_fmaf(f, s_l[q][w], ls[q]);
+            }
+            if (any_bad) ls[q] = __builtin_nanf("");
+        }
+    }
+    finish_partial<D, WAVES * 64, QG>(a, rt, M, ls, acc, epoch);
+}
+
+} // namespace va
