@@ -130,31 +130,44 @@ __device__ void finish_partial(const DecodeArgs& a, const Route& rt, const float
     const bool in_s = lane < S, own = lane == s;
     bool good = true;
     float lsum[QG];
+    // Every query slot's (m, l) of split `lane` (words 0, 1 of its partial) and
+    // the first round of this wave's o pairs are issued before any is used (the
+    // compiler barrier keeps them from being sunk to their uses), so the merge
+    // waits one round trip for all slots instead of one per slot. The words are
+    // taken out of each 16-byte vector right after its load (carrying the
+    // vector through the re-read loop was mis-compiled).
+    uint32_t mw[QG][4];
+    uint32_t op[QG][R][4];
+    auto part_rsrc = [&](int q) {
+        return make_rsrc(base + (size_t)q * S * PART_STRIDE, (uint32_t)S * PB);
+    };
+    auto load_round = [&](int q, const __amdgpu_buffer_rsrc_t& rp, int j0) {
+#pragma unroll
+        for (int i = 0; i < R; ++i) {
+            const int j = j0 + NW * i;           // wave-uniform: no load past the last split
+            if (j < S) {
+                const u32x4 x = ld128_dev(rp, (uint32_t)j * PB + 16u + (uint32_t)dp * 16u);
+                op[q][i][0] = x.x; op[q][i][1] = x.y; op[q][i][2] = x.z; op[q][i][3] = x.w;
+            }
+        }
+    };
+#pragma unroll
+    for (int q = 0; q < QG; ++q) {
+        if (q >= rt.nq) break;
+        const __amdgpu_buffer_rsrc_t rp = part_rsrc(q);
+        const u32x4 ml = ld128_dev(rp, (uint32_t)jl * PB);
+        mw[q][0] = ml.x; mw[q][1] = ml.y; mw[q][2] = ml.z; mw[q][3] = ml.w;
+        load_round(q, rp, w);
+    }
+    asm volatile("" ::: "memory");
 #pragma unroll
     for (int q = 0; q < QG; ++q) {
         lsum[q] = 1.f;
         if (q >= rt.nq) break;
-        const __amdgpu_buffer_rsrc_t rp = make_rsrc(base + (size_t)q * S * PART_STRIDE, (uint32_t)S * PB);
-        // (m, l) of split `lane` (words 0, 1 of its partial), and the first
-        // round of this wave's o pairs, issued together. The words are taken
-        // out of each 16-byte vector right after its load (carrying the vector
-        // through the re-read loop was mis-compiled).
-        const u32x4 ml = ld128_dev(rp, (uint32_t)jl * PB);
-        uint32_t op[R][4];
-        auto load_round = [&](int j0) {
-#pragma unroll
-            for (int i = 0; i < R; ++i) {
-                const int j = j0 + NW * i;       // wave-uniform: no load past the last split
-                if (j < S) {
-                    const u32x4 x = ld128_dev(rp, (uint32_t)j * PB + 16u + (uint32_t)dp * 16u);
-                    op[i][0] = x.x; op[i][1] = x.y; op[i][2] = x.z; op[i][3] = x.w;
-                }
-            }
-        };
-        load_round(w);
+        const __amdgpu_buffer_rsrc_t rp = part_rsrc(q);
         // Selection is branch-free and the rare re-read loop is wave-uniform (all
         // lanes run it, stale lanes take the new value).
-        uint32_t mv = ml.x, mt = ml.y, lv = ml.z, lt = ml.w;
+        uint32_t mv = mw[q][0], mt = mw[q][1], lv = mw[q][2], lt = mw[q][3];
         for (int k = 0; k < POLL_MAX; ++k) {     // rare: stores still in flight
             const bool need = in_s && !own && !(mt == tag && lt == tag);
             if (__builtin_amdgcn_ballot_w64(need) == 0) break;
@@ -175,7 +188,7 @@ __device__ void finish_partial(const DecodeArgs& a, const Route& rt, const float
         lsum[q] = wave_sum(wj * lj);
         float o0 = 0.f, o1 = 0.f;
         for (int j0 = w; j0 < S; j0 += NW * R) {
-            if (j0 != w) load_round(j0);
+            if (j0 != w) load_round(q, rp, j0);
 #pragma unroll
             for (int i = 0; i < R; ++i) {
                 const int j = j0 + NW * i;       // wave-uniform
@@ -185,7 +198,7 @@ __device__ void finish_partial(const DecodeArgs& a, const Route& rt, const float
                     v0 = s_own[q][2 * dp];
                     v1 = s_own[q][2 * dp + 1];
                 } else {
-                    uint32_t a0 = op[i][0], t0 = op[i][1], a1 = op[i][2], t1 = op[i][3];
+                    uint32_t a0 = op[q][i][0], t0 = op[q][i][1], a1 = op[q][i][2], t1 = op[q][i][3];
                     for (int k = 0; k < POLL_MAX; ++k) {
                         const bool need = !(t0 == tag && t1 == tag);
                         if (__builtin_amdgcn_ballot_w64(need) == 0) break;

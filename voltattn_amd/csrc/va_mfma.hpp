@@ -50,8 +50,16 @@ typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef int i32x2 __attribute__((ext_vector_type(2)));
 typedef __attribute__((address_space(3))) i32x2 lds_i32x2;
 
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+
 __device__ __forceinline__ f32x4 mfma_16x16x32(const f16x8& a, const f16x8& b, const f32x4& c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+// int8 x int8 -> int32, k = 64: lane l holds A[l%16][16(l/16)+e] and
+// B[16(l/16)+e][l%16] (e = 0..15, byte order; probed) and receives
+// D[4(l/16)+v][l%16].
+__device__ __forceinline__ i32x4 mfma_i8(const u32x4& a, const u32x4& b, const i32x4& c) {
+    return __builtin_amdgcn_mfma_i32_16x16x64_i8(__builtin_bit_cast(i32x4, a), __builtin_bit_cast(i32x4, b), c, 0, 0, 0);
 }
 
 // 8 int8 codes (two dwords, byte order) -> 8 exact fp16 values in the same order.
@@ -76,13 +84,13 @@ __global__ __launch_bounds__(WAVES * 64, 1) void decode_mfma(DecodeArgs a) {
     constexpr int TB   = TW * WAVES;
     constexpr int DQ   = D / 4;                  // row bytes per lane quarter (A operand)
     constexpr int KL   = DQ / 16;                // 16-byte K loads per block per lane
-    constexpr int NJ   = D / 32;                 // q.K MFMAs per block
+    constexpr int NJ   = D / 64;                 // q.K MFMAs (k = 64) per block and digit
     constexpr int NB   = D / 16;                 // P.V column blocks
     constexpr int VL   = TW * ROWB / (64 * 16);  // 16-byte V loads per lane per tile
     constexpr int VSTR = ROWB + 16;              // LDS row stride of the staged V tile
     constexpr int VROWS = TW + 4;                // rows 16..31 sit 4 slots further
     constexpr int SCE  = NG >= 2 ? TW * NG / 2 : TW;   // scale words (dwords, or halves at NG = 1)
-    static_assert(KL >= 1 && VL >= 1 && SCE <= 64, "tile shape");
+    static_assert(KL >= 1 && VL >= 1 && SCE <= 64 && NJ == KL, "tile shape");
 
     __shared__ __align__(16) uint8_t  s_v[WAVES][VROWS * VSTR];
     __shared__ __align__(16) uint32_t s_sc[WAVES][NG][TW];   // (k | v << 16) scale pairs
@@ -193,23 +201,60 @@ __global__ __launch_bounds__(WAVES * 64, 1) void decode_mfma(DecodeArgs a) {
 
         load_tile(0, ka, va_, ska, sva);
 
-        // q^T operand of the q.K products: column (cg, cq), k slots of quarter g
-        // are dimensions g*DQ + 8j + e. Zero outside group cg and for unused slots.
-        f16x8 qb[NJ];
+        // q^T operand of the q.K products: column (cg, cq); k slots of quarter g
+        // for MFMA j are dimensions g*DQ + 16j + e, zero outside group cg and for
+        // unused slots. q is exact as three balanced int8 digits of the integer
+        // round(q * 2^sh), sh per column putting max|q| in [2^21, 2^22) (every
+        // fp16 element within 2^-11 of the maximum is exact; below, the error is
+        // under 2^-23 of it), so each digit's dot with the int8 codes is exact
+        // in int32.
+        u32x4 qd[3][NJ];
+        float cf;                                 // qscale * 2^-sh of this column
         {
             const bool live = cq < rt.nq;
             const _Float16* qrow = reinterpret_cast<const _Float16*>(a.q) + (size_t)(rt.oh0 + (live ? cq : 0)) * D;
+            float qv[NJ][16];
+            float lmax = 0.f;
 #pragma unroll
             for (int j = 0; j < NJ; ++j) {
-                const int d0 = g * DQ + 8 * j;
+                const int d0 = g * DQ + 16 * j;
                 const bool use = live && (d0 / G) == cg;
-                const u32x4 w = *reinterpret_cast<const u32x4*>(qrow + d0);
-                const u32x4 z = use ? w : u32x4{0u, 0u, 0u, 0u};
-                qb[j] = __builtin_bit_cast(f16x8, z);
+                const u32x4 w0 = *reinterpret_cast<const u32x4*>(qrow + d0);
+                const u32x4 w1 = *reinterpret_cast<const u32x4*>(qrow + d0 + 8);
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    const uint32_t h0 = (e & 1) ? (w0[e >> 1] >> 16) : (w0[e >> 1] & 0xFFFFu);
+                    const uint32_t h1 = (e & 1) ? (w1[e >> 1] >> 16) : (w1[e >> 1] & 0xFFFFu);
+                    qv[j][e]     = use ? h2f(h0) : 0.f;
+                    qv[j][8 + e] = use ? h2f(h1) : 0.f;
+                    lmax = fmaxf(lmax, fmaxf(fabsf(qv[j][e]), fabsf(qv[j][8 + e])));
+                }
+            }
+            float cmax = fmaxf(lmax, swz_xor<16>(lmax));
+            cmax = fmaxf(cmax, lane_xor32(cmax));       // column maximum over the quarters
+            int sh = 0;
+            if (cmax > 0.f) sh = 22 - ((int)((__builtin_bit_cast(uint32_t, cmax) >> 23) & 0xFF) - 126);
+            const float up = __builtin_bit_cast(float, (uint32_t)(127 + sh) << 23);
+            cf = a.qscale * __builtin_bit_cast(float, (uint32_t)(127 - sh) << 23);
+#pragma unroll
+            for (int j = 0; j < NJ; ++j) {
+                uint32_t b[3][4] = {};
+#pragma unroll
+                for (int e = 0; e < 16; ++e) {
+                    const int qi = (int)__builtin_rintf(qv[j][e] * up);    // |qi| < 2^22
+                    const int d0 = (qi << 24) >> 24;
+                    const int r1 = (qi - d0) >> 8;
+                    const int d1 = (r1 << 24) >> 24;
+                    const int d2 = (r1 - d1) >> 8;                       // |d2| <= 64
+                    b[0][e >> 2] |= (uint32_t)(d0 & 0xFF) << (8 * (e & 3));
+                    b[1][e >> 2] |= (uint32_t)(d1 & 0xFF) << (8 * (e & 3));
+                    b[2][e >> 2] |= (uint32_t)(d2 & 0xFF) << (8 * (e & 3));
+                }
+#pragma unroll
+                for (int k = 0; k < 3; ++k) qd[k][j] = u32x4{b[k][0], b[k][1], b[k][2], b[k][3]};
             }
         }
         const uint32_t magic = [] { uint32_t m; VA_VGPR_CONST(m, 0x64646464); return m; }();
-        const float qs = a.qscale;
 
         // tr8 source row of this lane: tr row e = col/2 is position 16(e/4) + 4g + e%4,
         // half (col & 1) of a 16-byte column chunk.
@@ -248,43 +293,55 @@ __global__ __launch_bounds__(WAVES * 64, 1) void decode_mfma(DecodeArgs a) {
                     s_sc[wave][0][lane] = (sk & 0xFFFFu) | (sv << 16);
                 }
             }
-            // q.K: two 16-row blocks, NJ MFMAs each
-            f32x4 acc[2];
-#pragma unroll
-            for (int c = 0; c < 2; ++c) acc[c] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-            for (int j = 0; j < NJ; ++j)
-#pragma unroll
-                for (int c = 0; c < 2; ++c) {
-                    const u32x4& w = kk[c][j / 2];
-                    const f16x8 kf = q8_to_f16x8(w[2 * (j % 2)], w[2 * (j % 2) + 1], magic);
-                    acc[c] = mfma_16x16x32(kf, qb[j], acc[c]);
-                }
             __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
             __builtin_amdgcn_wave_barrier();
             __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+            // q.K: two 16-row blocks; per digit, NJ int8 MFMAs straight on the codes
+            i32x4 acc[3][2];
+#pragma unroll
+            for (int k = 0; k < 3; ++k)
+#pragma unroll
+                for (int c = 0; c < 2; ++c) acc[k][c] = i32x4{0, 0, 0, 0};
+#pragma unroll
+            for (int j = 0; j < NJ; ++j)
+#pragma unroll
+                for (int k = 0; k < 3; ++k)
+#pragma unroll
+                    for (int c = 0; c < 2; ++c) acc[k][c] = mfma_i8(kk[c][j], qd[k][j], acc[k][c]);
+            // V^T operands of the P.V products (independent of the softmax, so their
+            // LDS reads and unpack overlap the q.K MFMAs)
+            f16x8 vf[NB];
+#pragma unroll
+            for (int nb = 0; nb < NB; ++nb) {
+                const i32x2 t = __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_i32x2*)(sv_w + vrd + 16 * nb));
+                vf[nb] = q8_to_f16x8((uint32_t)t[0], (uint32_t)t[1], magic);
+            }
             // scale pairs of this lane's 8 positions (16c + 4g + v), group cg
             const u32x4 sc0 = *reinterpret_cast<const u32x4*>(&s_sc[wave][cg][4 * g]);
             const u32x4 sc1 = *reinterpret_cast<const u32x4*>(&s_sc[wave][cg][16 + 4 * g]);
             float x[8];
 #pragma unroll
-            for (int v = 0; v < 4; ++v) {
-                x[v]     = acc[0][v] * (h2f_lo(sc0[v]) * qs);
-                x[4 + v] = acc[1][v] * (h2f_lo(sc1[v]) * qs);
-            }
+            for (int c = 0; c < 2; ++c)
+#pragma unroll
+                for (int v = 0; v < 4; ++v) {
+                    // digits recombined: 2^16 acc2 + (2^8 acc1 + acc0), one rounding
+                    const float t = __builtin_fmaf((float)acc[2][c][v], 65536.f, (float)(acc[1][c][v] * 256 + acc[0][c][v]));
+                    x[4 * c + v] = t * (h2f_lo(c ? sc1[v] : sc0[v]) * cf);
+                }
             // sum the NG group columns of each query slot (row rotations by QP, 2QP)
 #pragma unroll
             for (int e = 0; e < 8; ++e) {
                 if constexpr (NG == 4) { x[e] += dpp<dpp_row_ror(8)>(x[e]); x[e] += dpp<dpp_row_ror(4)>(x[e]); }
                 if constexpr (NG == 2) { x[e] += dpp<dpp_row_ror(8)>(x[e]); }
             }
-            float tmax = -__builtin_inff();
+            if (rem < TW) {                       // partial tile: rows at or past rem are masked
 #pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                const int p = 16 * (e >> 2) + 4 * g + (e & 3);
-                if (p >= rem) x[e] = -__builtin_inff();
-                tmax = fmaxf(tmax, x[e]);
+                for (int e = 0; e < 8; ++e)
+                    if (16 * (e >> 2) + 4 * g + (e & 3) >= rem) x[e] = -__builtin_inff();
             }
+            float tmax = x[0];
+#pragma unroll
+            for (int e = 1; e < 8; ++e) tmax = fmaxf(tmax, x[e]);
             const bool raise = __builtin_amdgcn_ballot_w64(tmax > mq + RESCALE_SLACK) != 0;
             if (raise) {
                 // new maximum of each query slot: over its NG columns and the 4 quarters
@@ -331,13 +388,11 @@ __global__ __launch_bounds__(WAVES * 64, 1) void decode_mfma(DecodeArgs a) {
                 ahi[e] = hi;
                 alo[e] = (_Float16)(xv[e] - (float)hi);
             }
-            // P.V over NB column blocks: V^T operand from the staged tile
+            // P.V over NB column blocks
 #pragma unroll
             for (int nb = 0; nb < NB; ++nb) {
-                const i32x2 t = __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_i32x2*)(sv_w + vrd + 16 * nb));
-                const f16x8 vf = q8_to_f16x8((uint32_t)t[0], (uint32_t)t[1], magic);
-                o[nb] = mfma_16x16x32(ahi, vf, o[nb]);
-                o[nb] = mfma_16x16x32(alo, vf, o[nb]);
+                o[nb] = mfma_16x16x32(ahi, vf[nb], o[nb]);
+                o[nb] = mfma_16x16x32(alo, vf[nb], o[nb]);
             }
             __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
             __builtin_amdgcn_wave_barrier();
