@@ -37,6 +37,29 @@ LIB_PATH = Path(os.environ.get("VOLTATTN_LIB") or Path(__file__).resolve().paren
 if not LIB_PATH.exists():
     raise ImportError(
         f"{LIB_PATH} is not built; run `python voltattn_amd/build.py` (needs hipcc for gfx950)")
+
+
+def _bind_torch_hip_runtime() -> None:
+    """Load PyTorch-ROCm's own HIP runtime first, so this library binds to it.
+
+    A process holds one HIP runtime per loaded copy of libamdhip64; PyTorch-ROCm
+    ships its own and loads it by path. When this library has already brought in
+    the system ROCm runtime and initialised it, torch's later device init fails
+    ("No HIP GPUs are available"). Importing torch first avoids that by itself
+    (the library then binds to torch's already-loaded runtime by soname);
+    VOLTATTN_HIP_RUNTIME=torch does the same without importing torch."""
+    import importlib.util
+    spec = importlib.util.find_spec("torch")
+    if spec is None or not spec.submodule_search_locations:
+        raise ImportError("VOLTATTN_HIP_RUNTIME=torch but PyTorch is not installed")
+    rt = Path(list(spec.submodule_search_locations)[0]) / "lib" / "libamdhip64.so"
+    if not rt.exists():
+        raise ImportError(f"VOLTATTN_HIP_RUNTIME=torch but {rt} does not exist (not a ROCm build of torch?)")
+    C.CDLL(str(rt), mode=C.RTLD_GLOBAL)
+
+
+if os.environ.get("VOLTATTN_HIP_RUNTIME", "system") == "torch":
+    _bind_torch_hip_runtime()
 lib = C.CDLL(str(LIB_PATH))
 
 _P, _I, _SZ, _U64 = C.c_void_p, C.c_int, C.c_size_t, C.c_uint64

@@ -64,18 +64,19 @@ struct Route {
 // and issued its stores, so it is re-read (bounded) until it lands.
 //
 // The merge spreads the loads over all NT/64 waves (coherent loads are
-// serviced one instruction at a time): per query slot, lane j of every wave
-// reads split j's (m, l); wave w folds splits j = w, w + NW, ... in increasing
-// order into lane-pair columns (2i, 2i+1) with split j's weight read by
-// readlane; the NW wave sums are added in wave order through LDS. The order is
-// fixed, so the result does not depend on arrival order. A merged l of zero
+// serviced one instruction at a time) and runs the query slots side by side:
+// WQ = NW/QG waves per slot; lane j of each of them reads split j's (m, l),
+// and sub-wave sw folds splits j = sw, sw + WQ, ... in increasing order into
+// lane-pair columns (2i, 2i+1) with split j's weight read by readlane; the WQ
+// sub-wave sums are added in order through LDS. Each wave issues its (m, l)
+// and up to RB o-pair loads together, so the merge waits one round trip. The
+// order is fixed, so the result does not depend on arrival order. A merged l of zero
 // (no positions) gives a zero output; a non-finite one (an invalid input that
 // the kernel flagged with l = NaN) gives NaN. Needs S <= 64.
 template <int D, int NT, int QG>
 __device__ void finish_partial(const DecodeArgs& a, const Route& rt, const float (&M)[QG],
                                const float (&ls)[QG], const float (&acc)[QG], unsigned epoch) {
     constexpr int NW = NT / 64;
-    constexpr int R  = 4;                       // o-pair loads per wave per round
     constexpr uint32_t PB = PART_STRIDE * 8;    // bytes per partial (16-byte multiple)
     static_assert(PB % 16 == 0 && D + 2 <= PART_STRIDE, "partial layout");
     const int t = (int)threadIdx.x;
@@ -95,9 +96,19 @@ __device__ void finish_partial(const DecodeArgs& a, const Route& rt, const float
         }
         return;
     }
+    // The merge splits the NW waves over the query slots: WQ = NW / QG waves per
+    // slot (all waves on one slot when QG = 1); wave w merges slot w / WQ and
+    // folds its splits j = sw, sw + WQ, ... (sw = w % WQ) in increasing order.
+    constexpr int WQ = NW / QG;
+    static_assert(NW >= QG && NW % QG == 0, "whole waves per query slot");
+    // o-pair loads per wave per batch: a batch covers a slot's splits in the
+    // grouped forms; with one slot (the reference shape) a small batch keeps
+    // the register count, and so the occupancy, of the split pass.
+    constexpr int RB = QG > 1 ? 16 : 4;
     __shared__ int   s_last, s_bad;
     __shared__ float s_own[QG][D + 2];          // o[0..D), m, l of this group's partials
-    __shared__ float s_fold[QG][NW][D];
+    __shared__ float s_fold[QG][WQ][D];
+    __shared__ float s_lsum[QG];
     unsigned* ticket = g_tickets + ((size_t)a.ticket_slot * TICKET_MAXH + rt.mg) * TICKET_STRIDE;
     if (t == NT - 1)
         s_last = __hip_atomic_fetch_add(ticket, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
@@ -125,49 +136,36 @@ __device__ void finish_partial(const DecodeArgs& a, const Route& rt, const float
 
     const int w    = uniform(t >> 6);
     const int lane = t & 63;
+    const int qw   = w / WQ, sw = w - (w / WQ) * WQ;
     const int dp   = min(lane, D / 2 - 1);     // o pair of this lane: dims 2dp, 2dp + 1
     const int jl   = min(lane, S - 1);
     const bool in_s = lane < S, own = lane == s;
     bool good = true;
-    float lsum[QG];
-    // Every query slot's (m, l) of split `lane` (words 0, 1 of its partial) and
-    // the first round of this wave's o pairs are issued before any is used (the
-    // compiler barrier keeps them from being sunk to their uses), so the merge
-    // waits one round trip for all slots instead of one per slot. The words are
-    // taken out of each 16-byte vector right after its load (carrying the
-    // vector through the re-read loop was mis-compiled).
-    uint32_t mw[QG][4];
-    uint32_t op[QG][R][4];
-    auto part_rsrc = [&](int q) {
-        return make_rsrc(base + (size_t)q * S * PART_STRIDE, (uint32_t)S * PB);
-    };
-    auto load_round = [&](int q, const __amdgpu_buffer_rsrc_t& rp, int j0) {
+    if (qw < rt.nq) {                            // wave-uniform
+        const __amdgpu_buffer_rsrc_t rp = make_rsrc(base + (size_t)qw * S * PART_STRIDE, (uint32_t)S * PB);
+        const int nsw = (S - sw + WQ - 1) / WQ;  // splits folded by this wave
+        uint32_t op[RB][4];
+        auto load_batch = [&](int b0) {
 #pragma unroll
-        for (int i = 0; i < R; ++i) {
-            const int j = j0 + NW * i;           // wave-uniform: no load past the last split
-            if (j < S) {
-                const u32x4 x = ld128_dev(rp, (uint32_t)j * PB + 16u + (uint32_t)dp * 16u);
-                op[q][i][0] = x.x; op[q][i][1] = x.y; op[q][i][2] = x.z; op[q][i][3] = x.w;
+            for (int i = 0; i < RB; ++i) {
+                const int j = sw + WQ * (b0 + i);  // wave-uniform: no load past the last split
+                if (b0 + i < nsw) {
+                    const u32x4 x = ld128_dev(rp, (uint32_t)j * PB + 16u + (uint32_t)dp * 16u);
+                    op[i][0] = x.x; op[i][1] = x.y; op[i][2] = x.z; op[i][3] = x.w;
+                }
             }
-        }
-    };
-#pragma unroll
-    for (int q = 0; q < QG; ++q) {
-        if (q >= rt.nq) break;
-        const __amdgpu_buffer_rsrc_t rp = part_rsrc(q);
+        };
+        // (m, l) of split `lane` (words 0, 1 of its partial) and the first batch
+        // of o pairs are issued together (the compiler barrier keeps the loads
+        // from being sunk to their uses). The words are taken out of each 16-byte
+        // vector right after its load (carrying the vector through the re-read
+        // loop was mis-compiled).
         const u32x4 ml = ld128_dev(rp, (uint32_t)jl * PB);
-        mw[q][0] = ml.x; mw[q][1] = ml.y; mw[q][2] = ml.z; mw[q][3] = ml.w;
-        load_round(q, rp, w);
-    }
-    asm volatile("" ::: "memory");
-#pragma unroll
-    for (int q = 0; q < QG; ++q) {
-        lsum[q] = 1.f;
-        if (q >= rt.nq) break;
-        const __amdgpu_buffer_rsrc_t rp = part_rsrc(q);
+        uint32_t mv = ml.x, mt = ml.y, lv = ml.z, lt = ml.w;
+        load_batch(0);
+        asm volatile("" ::: "memory");
         // Selection is branch-free and the rare re-read loop is wave-uniform (all
         // lanes run it, stale lanes take the new value).
-        uint32_t mv = mw[q][0], mt = mw[q][1], lv = mw[q][2], lt = mw[q][3];
         for (int k = 0; k < POLL_MAX; ++k) {     // rare: stores still in flight
             const bool need = in_s && !own && !(mt == tag && lt == tag);
             if (__builtin_amdgcn_ballot_w64(need) == 0) break;
@@ -180,25 +178,25 @@ __device__ void finish_partial(const DecodeArgs& a, const Route& rt, const float
             lt = need ? rlt : lt;
         }
         good = good && (!in_s || own || (mt == tag && lt == tag));
-        const float own_m = s_own[q][D], own_l = s_own[q][D + 1];
+        const float own_m = s_own[qw][D], own_l = s_own[qw][D + 1];
         const float mj = !in_s ? -__builtin_inff() : own ? own_m : __builtin_bit_cast(float, mv);
         const float lj = !in_s ? 0.f : own ? own_l : __builtin_bit_cast(float, lv);
         const float mx = wave_max(mj);
         const float wj = fast_exp2(mj - mx);    // weight of split `lane` (0 past S)
-        lsum[q] = wave_sum(wj * lj);
+        const float lsum = wave_sum(wj * lj);
         float o0 = 0.f, o1 = 0.f;
-        for (int j0 = w; j0 < S; j0 += NW * R) {
-            if (j0 != w) load_round(q, rp, j0);
+        for (int b0 = 0; b0 < nsw; b0 += RB) {
+            if (b0 != 0) load_batch(b0);         // splits beyond the first batch (S > RB * WQ)
 #pragma unroll
-            for (int i = 0; i < R; ++i) {
-                const int j = j0 + NW * i;       // wave-uniform
-                if (j >= S) break;
+            for (int i = 0; i < RB; ++i) {
+                if (b0 + i >= nsw) break;        // wave-uniform
+                const int j = sw + WQ * (b0 + i);
                 float v0, v1;
                 if (j == s) {                    // wave-uniform
-                    v0 = s_own[q][2 * dp];
-                    v1 = s_own[q][2 * dp + 1];
+                    v0 = s_own[qw][2 * dp];
+                    v1 = s_own[qw][2 * dp + 1];
                 } else {
-                    uint32_t a0 = op[q][i][0], t0 = op[q][i][1], a1 = op[q][i][2], t1 = op[q][i][3];
+                    uint32_t a0 = op[i][0], t0 = op[i][1], a1 = op[i][2], t1 = op[i][3];
                     for (int k = 0; k < POLL_MAX; ++k) {
                         const bool need = !(t0 == tag && t1 == tag);
                         if (__builtin_amdgcn_ballot_w64(need) == 0) break;
@@ -221,9 +219,10 @@ __device__ void finish_partial(const DecodeArgs& a, const Route& rt, const float
             }
         }
         if (lane < D / 2) {
-            s_fold[q][w][2 * lane]     = o0;
-            s_fold[q][w][2 * lane + 1] = o1;
+            s_fold[qw][sw][2 * lane]     = o0;
+            s_fold[qw][sw][2 * lane + 1] = o1;
         }
+        if (sw == 0 && lane == 0) s_lsum[qw] = lsum;
     }
     // A lost partial (never observed within the poll bound) shows as NaN.
     if (__builtin_amdgcn_ballot_w64(!good) != 0 && lane == 0) s_bad = 1;
@@ -234,8 +233,8 @@ __device__ void finish_partial(const DecodeArgs& a, const Route& rt, const float
             if (q >= rt.nq) break;
             float o = 0.f;
 #pragma unroll
-            for (int v = 0; v < NW; ++v) o += s_fold[q][v][t];
-            const float r = lsum[q] == 0.f ? 0.f : o / lsum[q];
+            for (int v = 0; v < WQ; ++v) o += s_fold[q][v][t];
+            const float r = s_lsum[q] == 0.f ? 0.f : o / s_lsum[q];
             a.out[(size_t)(rt.oh0 + q) * D + t] = s_bad ? (uint16_t)0x7E00u : f2h_rne(r);
         }
     }
