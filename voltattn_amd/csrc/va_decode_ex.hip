@@ -28,7 +28,7 @@ namespace va {
 #define VA_EX_MODE 2
 #endif
 
-// Matrix-core form (va_mfma.hpp) for q8 rows with two or more query slots:
+// Matrix-core form (va_mfma.hpp) for q8 and q4 rows with two or more query slots:
 // MFMA_WAVES waves per work-group, 32-row wave tiles. VA_MFMA=0 in the
 // environment selects the VALU form instead (a tuning switch, read once).
 #ifndef VA_MFMA_WAVES
@@ -42,17 +42,19 @@ static bool mfma_on() {
     return on;
 }
 
-static bool mfma_form(int kind, int qg) { return kind == KQ8 && qg >= 2 && mfma_on(); }
+static bool mfma_kind(int kind) { return (kind == KQ8 || kind == KQ4) && mfma_on(); }
+static bool mfma_form(int kind, int qg) { return mfma_kind(kind) && qg >= 2; }
 
 // Query slots per work-group, per kind: the largest QG whose 8-wave form (two
 // waves per SIMD) fits in 256 VGPRs. Measured on MI355X (Hq/Hkv = 32/8, 64/8,
 // 28/4 at L = 16K-64K): QG = 4 at two waves per SIMD beats QG = 8 at one for
 // f16 and q8 (groups of 8 run as two sub-groups, 12-38% faster), and q4 is
-// fastest at QG = 2 (QG = 4 spills at two waves per SIMD). VA_EX_QMAX=1|2|4
-// lowers the cap (a tuning switch, read once).
+// fastest at QG = 2 (QG = 4 spills at two waves per SIMD). The matrix-core
+// form carries 4 slots for q4 too. VA_EX_QMAX=1|2|4 lowers the cap (a tuning
+// switch, read once).
 int max_query_slots(int kind) {
     static const int cap = [] { const char* e = std::getenv("VA_EX_QMAX"); return e ? std::atoi(e) : 0; }();
-    const int q = (kind == KF16 || kind == KQ8) ? 4 : 2;
+    const int q = (kind == KF16 || kind == KQ8 || mfma_kind(kind)) ? 4 : 2;
     return (cap == 1 || cap == 2 || cap == 4) ? std::min(q, cap) : q;
 }
 
@@ -117,20 +119,21 @@ int tile_positions_ex(int kind, int D) {
     switch (kind) {
         case KF16: return D == 128 ? max_tile<KF16, 128>() : max_tile<KF16, 64>();
         case KQ8:  return std::max(MFMA_TILE, D == 128 ? max_tile<KQ8, 128>() : max_tile<KQ8, 64>());
-        case KQ4:  return D == 128 ? max_tile<KQ4, 128>()  : max_tile<KQ4, 64>();
+        case KQ4:  return std::max(MFMA_TILE, D == 128 ? max_tile<KQ4, 128>() : max_tile<KQ4, 64>());
         default:   return D == 128 ? max_tile<KQ3, 128>()  : max_tile<KQ3, 64>();
     }
 }
 
 template <int KIND, int D, int G, int QG, bool PAGED>
 static hipError_t launch_ex(int groups, const DecodeArgs& a, hipStream_t st) {
-    if constexpr (KIND == KQ8 && QG >= 2) {
+    if constexpr ((KIND == KQ8 || KIND == KQ4) && QG >= 2) {
         if (mfma_on()) {
             hipLaunchKernelGGL((decode_mfma<KIND, D, G, MFMA_WAVES, QG, PAGED>),
                                dim3((unsigned)(groups * a.S)), dim3(MFMA_WAVES * 64), 0, st, a);
             return hipGetLastError();
         }
     }
+    if constexpr (KIND == KQ4 && QG > 2) return hipErrorInvalidValue;   // matrix-core form only
     using Cfg = ExCfg<KIND, QG>;
     constexpr int U = ex_unroll<KIND, D, QG>();
     static_assert(Tile<KIND, D>::PPW * U <= 64, "a wave tile must fit the smallest page");
@@ -147,7 +150,7 @@ static hipError_t launch_qg(int qg, int groups, const DecodeArgs& a, hipStream_t
             else return hipErrorInvalidValue;       // QG = 1 contiguous: va_decode.hip
         case 2: return launch_ex<KIND, D, G, 2, PAGED>(groups, a, st);
         case 4:
-            if constexpr (KIND == KF16 || KIND == KQ8) return launch_ex<KIND, D, G, 4, PAGED>(groups, a, st);
+            if constexpr (KIND == KF16 || KIND == KQ8 || KIND == KQ4) return launch_ex<KIND, D, G, 4, PAGED>(groups, a, st);
             else return hipErrorInvalidValue;
         default: return hipErrorInvalidValue;          // above max_query_slots(kind)
     }

@@ -62,6 +62,29 @@ __device__ __forceinline__ i32x4 mfma_i8(const u32x4& a, const u32x4& b, const i
     return __builtin_amdgcn_mfma_i32_16x16x64_i8(__builtin_bit_cast(i32x4, a), __builtin_bit_cast(i32x4, b), c, 0, 0, 0);
 }
 
+__device__ __forceinline__ u32x2 ld64(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+    return __builtin_amdgcn_raw_buffer_load_b64(r, voff, sgpr(soff), VA_LOAD_AUX);
+}
+
+// 8 bytes of q4 codes (two dwords, byte order) -> the 8 low nibbles as exact fp16
+// v = n - 8, and the 8 high nibbles as exact fp16 16v (masked in place under the
+// 1024.0 magic: 1024 + 16n - 1152).
+__device__ __forceinline__ void q4_to_f16x8(uint32_t w0, uint32_t w1, uint32_t magic, f16x8& lo, f16x8& hi) {
+    const h2 blo = hh(1032.f, 1032.f), bhi = hh(1152.f, 1152.f);
+    const uint32_t l0 = w0 & 0x0F0F0F0Fu, l1 = w1 & 0x0F0F0F0Fu;
+    const uint32_t u0 = w0 & 0xF0F0F0F0u, u1 = w1 & 0xF0F0F0F0u;
+    const h2 a0 = as_h2(__builtin_amdgcn_perm(magic, l0, 0x04010400u)) - blo;
+    const h2 a1 = as_h2(__builtin_amdgcn_perm(magic, l0, 0x04030402u)) - blo;
+    const h2 a2 = as_h2(__builtin_amdgcn_perm(magic, l1, 0x04010400u)) - blo;
+    const h2 a3 = as_h2(__builtin_amdgcn_perm(magic, l1, 0x04030402u)) - blo;
+    const h2 b0 = as_h2(__builtin_amdgcn_perm(magic, u0, 0x04010400u)) - bhi;
+    const h2 b1 = as_h2(__builtin_amdgcn_perm(magic, u0, 0x04030402u)) - bhi;
+    const h2 b2 = as_h2(__builtin_amdgcn_perm(magic, u1, 0x04010400u)) - bhi;
+    const h2 b3 = as_h2(__builtin_amdgcn_perm(magic, u1, 0x04030402u)) - bhi;
+    lo = f16x8{a0.x, a0.y, a1.x, a1.y, a2.x, a2.y, a3.x, a3.y};
+    hi = f16x8{b0.x, b0.y, b1.x, b1.y, b2.x, b2.y, b3.x, b3.y};
+}
+
 // 8 int8 codes (two dwords, byte order) -> 8 exact fp16 values in the same order.
 __device__ __forceinline__ f16x8 q8_to_f16x8(uint32_t w0, uint32_t w1, uint32_t magic) {
     const uint32_t u0 = w0 ^ 0x80808080u, u1 = w1 ^ 0x80808080u;
@@ -75,22 +98,24 @@ __device__ __forceinline__ f16x8 q8_to_f16x8(uint32_t w0, uint32_t w1, uint32_t 
 
 template <int KIND, int D, int G, int WAVES, int QG, bool PAGED>
 __global__ __launch_bounds__(WAVES * 64, 1) void decode_mfma(DecodeArgs a) {
-    static_assert(KIND == KQ8, "matrix-core form: q8 rows");
-    constexpr int ROWB = D;                      // q8: one byte per element
+    static_assert(KIND == KQ8 || KIND == KQ4, "matrix-core form: q8 and q4 rows");
+    constexpr bool Q4  = KIND == KQ4;
+    constexpr int ROWB = Q4 ? D / 2 : D;         // bytes per row
     constexpr int NG   = D / G;                  // scale groups per row (1, 2, 4)
     constexpr int QP   = 16 / NG;                // column slots per scale group
     static_assert(QG >= 1 && QG <= QP, "query slots per work-group");
     constexpr int TW   = 32;                     // rows per wave tile (two 16-row blocks)
     constexpr int TB   = TW * WAVES;
-    constexpr int DQ   = D / 4;                  // row bytes per lane quarter (A operand)
-    constexpr int KL   = DQ / 16;                // 16-byte K loads per block per lane
+    constexpr int DQ   = ROWB / 4;               // row bytes per lane quarter (A operand)
+    constexpr int KL   = DQ >= 16 ? DQ / 16 : 1; // K loads per block per lane (16 B; q4 at D = 64: 8 B)
     constexpr int NJ   = D / 64;                 // q.K MFMAs (k = 64) per block and digit
-    constexpr int NB   = D / 16;                 // P.V column blocks
+    constexpr int NB   = D / 16;                 // P.V column blocks (16 dimensions each)
+    constexpr int NC   = ROWB / 16;              // 16-byte column chunks of a V row
     constexpr int VL   = TW * ROWB / (64 * 16);  // 16-byte V loads per lane per tile
     constexpr int VSTR = ROWB + 16;              // LDS row stride of the staged V tile
     constexpr int VROWS = TW + 4;                // rows 16..31 sit 4 slots further
     constexpr int SCE  = NG >= 2 ? TW * NG / 2 : TW;   // scale words (dwords, or halves at NG = 1)
-    static_assert(KL >= 1 && VL >= 1 && SCE <= 64 && NJ == KL, "tile shape");
+    static_assert(VL >= 1 && SCE <= 64 && (Q4 ? NC * 2 == NB : (NC == NB && NJ == KL)), "tile shape");
 
     __shared__ __align__(16) uint8_t  s_v[WAVES][VROWS * VSTR];
     __shared__ __align__(16) uint32_t s_sc[WAVES][NG][TW];   // (k | v << 16) scale pairs
@@ -191,8 +216,14 @@ __global__ __launch_bounds__(WAVES * 64, 1) void decode_mfma(DecodeArgs a) {
 #pragma unroll
             for (int c = 0; c < 2; ++c)
 #pragma unroll
-                for (int i = 0; i < KL; ++i)
-                    kk[c][i] = ld128(tk, koff + (uint32_t)(c * 16 * ROWB + 16 * i), tpos * ROWB);
+                for (int i = 0; i < KL; ++i) {
+                    if constexpr (DQ >= 16) {
+                        kk[c][i] = ld128(tk, koff + (uint32_t)(c * 16 * ROWB + 16 * i), tpos * ROWB);
+                    } else {
+                        const u32x2 h = ld64(tk, koff + (uint32_t)(c * 16 * ROWB), tpos * ROWB);
+                        kk[c][i] = u32x4{h.x, h.y, 0u, 0u};
+                    }
+                }
 #pragma unroll
             for (int i = 0; i < VL; ++i)
                 vv[i] = ld128(tv, (uint32_t)(16 * (64 * i + lane)), tpos * ROWB);
@@ -210,24 +241,22 @@ __global__ __launch_bounds__(WAVES * 64, 1) void decode_mfma(DecodeArgs a) {
         // in int32.
         u32x4 qd[3][NJ];
         float cf;                                 // qscale * 2^-sh of this column
+        int   qoff[3] = {0, 0, 0};                // q4: -8 * (column sum of each digit)
         {
-            const bool live = cq < rt.nq;
-            const _Float16* qrow = reinterpret_cast<const _Float16*>(a.q) + (size_t)(rt.oh0 + (live ? cq : 0)) * D;
-            float qv[NJ][16];
+            constexpr int EPQ = D / 4;            // dimensions of a lane quarter
+            const int e0 = g * EPQ;               // they all lie in scale group e0 / G
+            const bool use = cq < rt.nq && e0 / G == cg;
+            const _Float16* qrow = reinterpret_cast<const _Float16*>(a.q) + (size_t)(rt.oh0 + (cq < rt.nq ? cq : 0)) * D;
+            float qe[EPQ];
             float lmax = 0.f;
 #pragma unroll
-            for (int j = 0; j < NJ; ++j) {
-                const int d0 = g * DQ + 16 * j;
-                const bool use = live && (d0 / G) == cg;
-                const u32x4 w0 = *reinterpret_cast<const u32x4*>(qrow + d0);
-                const u32x4 w1 = *reinterpret_cast<const u32x4*>(qrow + d0 + 8);
+            for (int i = 0; i < EPQ / 8; ++i) {
+                const u32x4 w = *reinterpret_cast<const u32x4*>(qrow + e0 + 8 * i);
 #pragma unroll
                 for (int e = 0; e < 8; ++e) {
-                    const uint32_t h0 = (e & 1) ? (w0[e >> 1] >> 16) : (w0[e >> 1] & 0xFFFFu);
-                    const uint32_t h1 = (e & 1) ? (w1[e >> 1] >> 16) : (w1[e >> 1] & 0xFFFFu);
-                    qv[j][e]     = use ? h2f(h0) : 0.f;
-                    qv[j][8 + e] = use ? h2f(h1) : 0.f;
-                    lmax = fmaxf(lmax, fmaxf(fabsf(qv[j][e]), fabsf(qv[j][8 + e])));
+                    const uint32_t h = (e & 1) ? (w[e >> 1] >> 16) : (w[e >> 1] & 0xFFFFu);
+                    qe[8 * i + e] = use ? h2f(h) : 0.f;
+                    lmax = fmaxf(lmax, fabsf(qe[8 * i + e]));
                 }
             }
             float cmax = fmaxf(lmax, swz_xor<16>(lmax));
@@ -236,22 +265,37 @@ __global__ __launch_bounds__(WAVES * 64, 1) void decode_mfma(DecodeArgs a) {
             if (cmax > 0.f) sh = 22 - ((int)((__builtin_bit_cast(uint32_t, cmax) >> 23) & 0xFF) - 126);
             const float up = __builtin_bit_cast(float, (uint32_t)(127 + sh) << 23);
             cf = a.qscale * __builtin_bit_cast(float, (uint32_t)(127 - sh) << 23);
+            float dsum[3] = {0.f, 0.f, 0.f};
 #pragma unroll
             for (int j = 0; j < NJ; ++j) {
-                uint32_t b[3][4] = {};
+                uint32_t bq[3][4] = {};
 #pragma unroll
                 for (int e = 0; e < 16; ++e) {
-                    const int qi = (int)__builtin_rintf(qv[j][e] * up);    // |qi| < 2^22
+                    // k slot e of MFMA j: q8 dimension 16j + e of the quarter; q4 the
+                    // nibble order of the A operand (low nibbles, then high nibbles)
+                    const int de = !Q4 ? 16 * j + e : (D == 128 ? 2 * e + j : (e < 8 ? 2 * e : 2 * (e - 8) + 1));
+                    const int qi = (int)__builtin_rintf(qe[de] * up);        // |qi| < 2^22
                     const int d0 = (qi << 24) >> 24;
                     const int r1 = (qi - d0) >> 8;
                     const int d1 = (r1 << 24) >> 24;
-                    const int d2 = (r1 - d1) >> 8;                       // |d2| <= 64
-                    b[0][e >> 2] |= (uint32_t)(d0 & 0xFF) << (8 * (e & 3));
-                    b[1][e >> 2] |= (uint32_t)(d1 & 0xFF) << (8 * (e & 3));
-                    b[2][e >> 2] |= (uint32_t)(d2 & 0xFF) << (8 * (e & 3));
+                    const int d2 = (r1 - d1) >> 8;                           // |d2| <= 64
+                    bq[0][e >> 2] |= (uint32_t)(d0 & 0xFF) << (8 * (e & 3));
+                    bq[1][e >> 2] |= (uint32_t)(d1 & 0xFF) << (8 * (e & 3));
+                    bq[2][e >> 2] |= (uint32_t)(d2 & 0xFF) << (8 * (e & 3));
+                    dsum[0] += (float)d0;
+                    dsum[1] += (float)d1;
+                    dsum[2] += (float)d2;
                 }
 #pragma unroll
-                for (int k = 0; k < 3; ++k) qd[k][j] = u32x4{b[k][0], b[k][1], b[k][2], b[k][3]};
+                for (int k = 0; k < 3; ++k) qd[k][j] = u32x4{bq[k][0], bq[k][1], bq[k][2], bq[k][3]};
+            }
+            if constexpr (Q4) {                   // codes enter as n = v + 8
+#pragma unroll
+                for (int k = 0; k < 3; ++k) {
+                    float cs = dsum[k] + swz_xor<16>(dsum[k]);
+                    cs += lane_xor32(cs);
+                    qoff[k] = -8 * (int)cs;
+                }
             }
         }
         const uint32_t magic = [] { uint32_t m; VA_VGPR_CONST(m, 0x64646464); return m; }();
@@ -301,20 +345,31 @@ __global__ __launch_bounds__(WAVES * 64, 1) void decode_mfma(DecodeArgs a) {
 #pragma unroll
             for (int k = 0; k < 3; ++k)
 #pragma unroll
-                for (int c = 0; c < 2; ++c) acc[k][c] = i32x4{0, 0, 0, 0};
+                for (int c = 0; c < 2; ++c) acc[k][c] = i32x4{qoff[k], qoff[k], qoff[k], qoff[k]};
 #pragma unroll
             for (int j = 0; j < NJ; ++j)
 #pragma unroll
-                for (int k = 0; k < 3; ++k)
+                for (int c = 0; c < 2; ++c) {
+                    u32x4 kop;                    // A operand: int8 codes of 16 k slots
+                    if constexpr (!Q4) {
+                        kop = kk[c][j];
+                    } else if constexpr (D == 128) {
+                        kop = j == 0 ? (kk[c][0] & 0x0F0F0F0Fu) : ((kk[c][0] >> 4) & 0x0F0F0F0Fu);
+                    } else {
+                        const uint32_t w0 = kk[c][0].x, w1 = kk[c][0].y;
+                        kop = u32x4{w0 & 0x0F0F0F0Fu, w1 & 0x0F0F0F0Fu, (w0 >> 4) & 0x0F0F0F0Fu, (w1 >> 4) & 0x0F0F0F0Fu};
+                    }
 #pragma unroll
-                    for (int c = 0; c < 2; ++c) acc[k][c] = mfma_i8(kk[c][j], qd[k][j], acc[k][c]);
+                    for (int k = 0; k < 3; ++k) acc[k][c] = mfma_i8(kop, qd[k][j], acc[k][c]);
+                }
             // V^T operands of the P.V products (independent of the softmax, so their
             // LDS reads and unpack overlap the q.K MFMAs)
             f16x8 vf[NB];
 #pragma unroll
-            for (int nb = 0; nb < NB; ++nb) {
-                const i32x2 t = __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_i32x2*)(sv_w + vrd + 16 * nb));
-                vf[nb] = q8_to_f16x8((uint32_t)t[0], (uint32_t)t[1], magic);
+            for (int c16 = 0; c16 < NC; ++c16) {
+                const i32x2 t = __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_i32x2*)(sv_w + vrd + 16 * c16));
+                if constexpr (!Q4) vf[c16] = q8_to_f16x8((uint32_t)t[0], (uint32_t)t[1], magic);
+                else q4_to_f16x8((uint32_t)t[0], (uint32_t)t[1], magic, vf[2 * c16], vf[2 * c16 + 1]);
             }
             // scale pairs of this lane's 8 positions (16c + 4g + v), group cg
             const u32x4 sc0 = *reinterpret_cast<const u32x4*>(&s_sc[wave][cg][4 * g]);
@@ -425,8 +480,11 @@ __global__ __launch_bounds__(WAVES * 64, 1) void decode_mfma(DecodeArgs a) {
         const float f  = __builtin_bit_cast(float, (uint32_t)(127 - (int)er) << 23);
 #pragma unroll
         for (int nb = 0; nb < NB; ++nb) {
-            const int d = 16 * nb + col;
-            if (r / QP == d / G && r % QP < QG) s_red[r % QP][wave][d] = o[nb][v] * f;
+            // q8: block nb is dimensions 16nb + col; q4: byte column 16(nb/2) + col,
+            // low nibble (even dimension) or high nibble (odd, accumulated as 16v)
+            const int d = !Q4 ? 16 * nb + col : 2 * (16 * (nb >> 1) + col) + (nb & 1);
+            const float fh = (Q4 && (nb & 1)) ? f * 0.0625f : f;
+            if (r / QP == d / G && r % QP < QG) s_red[r % QP][wave][d] = o[nb][v] * fh;
         }
     }
     bool any_bad = false;
