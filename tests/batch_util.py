@@ -107,3 +107,24 @@ class PagedBatch:
         for d in self.bufs:
             d.free()
         self.bufs = []
+
+
+def kv_from_values(fmt: va.Fmt, xk: np.ndarray, xv: np.ndarray, G: int) -> dict:
+    """K/V of chosen fp32 values [Hkv][L][D]: the reference's quantizer (quantize(),
+    src/voltattn.cu:705-745) for the quantized formats, fp16 rounding for f16."""
+    Hkv, L, D = xk.shape
+    bits = va.fmt_bits(fmt)
+    rb = va.row_bytes(fmt, D)
+    out = {"ksc": None, "vsc": None}
+    for name, x in (("k", xk), ("v", xv)):
+        x = np.ascontiguousarray(x, np.float32)
+        if bits == 16:
+            h = x.astype(np.float16)
+            out[name + "pay"] = h.view(np.uint8).reshape(Hkv, L, rb)
+            out[name + "d"] = h.astype(np.float32).ravel()
+        else:
+            data, scale = oracle.quantize(x, D, G, bits)
+            out[name + "pay"] = data.reshape(Hkv, L, rb)
+            out[name + "sc"] = scale.reshape(Hkv, L, D // G)
+            out[name + "d"] = oracle.dequant(data, scale, Hkv * L, D, G, bits)
+    return out
