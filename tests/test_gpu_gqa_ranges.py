@@ -23,10 +23,10 @@ from tests.numerics import tight_bound
 pytestmark = pytest.mark.gpu
 
 TILED = [va.Fmt.F16M, va.Fmt.Q8M, va.Fmt.Q4M, va.Fmt.Q3M]
-Hq, Hkv, L, D, G = 8, 2, 3000, 128, 32
+L, D, G = 3000, 128, 32
 
 
-def _values(kind: str, rng):
+def _values(kind: str, rng, Hq: int, Hkv: int):
     xk = rng.standard_normal((Hkv, L, D)).astype(np.float32)
     xv = rng.standard_normal((Hkv, L, D)).astype(np.float32)
     q = rng.standard_normal((Hq, D)).astype(np.float32)
@@ -60,12 +60,15 @@ def _values(kind: str, rng):
 @pytest.mark.parametrize("fmt", TILED, ids=lambda f: f.label)
 @pytest.mark.parametrize("kind", ["row_scales", "group_scales", "sharp", "flat", "rising",
                                   "zero_groups", "big_v"])
-def test_gqa_value_ranges(fmt, kind):
-    rng = np.random.default_rng(zlib.crc32(f"{kind}/{fmt.label}".encode()))
-    xk, xv, q = _values(kind, rng)
+@pytest.mark.parametrize("heads", [(8, 2), (4, 4)], ids=lambda h: f"Hq{h[0]}-Hkv{h[1]}")
+def test_gqa_value_ranges(fmt, kind, heads):
+    """Hq = Hkv is the reference shape (va_decode_gqa forwards it to va_decode)."""
+    Hq, Hkv = heads
+    rng = np.random.default_rng(zlib.crc32(f"{kind}/{fmt.label}/{Hq}".encode()))
+    xk, xv, q = _values(kind, rng, Hq, Hkv)
     c = batch_util.kv_from_values(fmt, xk, xv, G)
     qh = batch_util.f16(q.ravel()).reshape(Hq, D)
-    print(f"gqa range {fmt.label} {kind}", flush=True)
+    print(f"gqa range {fmt.label} {kind} Hq={Hq} Hkv={Hkv}", flush=True)
     bufs = []
     try:
         dev = lambda a: bufs.append(va.DeviceBuffer.from_array(a)) or bufs[-1].ptr
@@ -90,13 +93,13 @@ def test_gqa_value_ranges(fmt, kind):
     assert ok, (fmt.label, kind, maxerr)
     tb = tight_bound(ref)
     print(f"  err/tight max {float((np.abs(got - ref) / tb).max()):.3g}", flush=True)
-    bound = tb + _fp32_score_term(c, qh).ravel()
+    bound = tb + _fp32_score_term(c, qh, Hq, Hkv).ravel()
     bad = np.abs(got - ref) > bound
     assert not bad.any(), (fmt.label, kind, int(bad.sum()), float(np.abs(got - ref).max()),
                            float((np.abs(got - ref) / bound).max()))
 
 
-def _fp32_score_term(c, qh):
+def _fp32_score_term(c, qh, Hq, Hkv):
     """Per query head: 2 * max|v| * 8 ulp(fp32) * ln2 * max_j sum_d |q_d k_jd| * log2(e)/sqrt(D)."""
     kd = c["kd"].reshape(Hkv, L, D).astype(np.float64)
     vd = c["vd"].reshape(Hkv, L, D).astype(np.float64)
