@@ -2,6 +2,8 @@
 // over the C ABI: correctness selftest, read-bandwidth probe and benchmark.
 //
 //   voltattn [--selftest]   42-case selftest at G=64 (+ the quantized cases at G=32)
+//   voltattn --selftest-ex  grouped-query, paged and append cases through the
+//                           C++ mirror (voltattn.hpp), 42 cases
 //   voltattn --probe        HBM read ceiling
 //   voltattn --bench        selftest gate, probe, then the format x L table
 //
@@ -91,6 +93,244 @@ int selftest() {
     }
     if (fails) { std::printf("%d of %d case(s) FAILED\n", fails, n); return 1; }
     std::printf("all %d cases passed\n", n);
+    return 0;
+}
+
+// ------------------------------------------------------- grouped / paged --
+// Grouped-query, paged and append paths through the C++ mirror (no reference
+// counterpart: its README.md:205-206 lists GQA and paged KV as missing). K/V
+// rows are seeded fp16 draws, quantized by the oracle; the expected output is
+// the oracle's double reference per query head over the dequantized rows, the
+// gate the reference's (src/voltattn.cu:903).
+std::vector<uint16_t> draw_f16(size_t n, uint32_t seed) {
+    oracle::Mt19937 g(seed);
+    oracle::NormalPolar nd;
+    std::vector<uint16_t> x(n);
+    for (auto& h : x) h = oracle::f32_to_f16(nd.next(g));
+    return x;
+}
+
+// fp16 rows [rows][D] in a format's row layout, and their dequantized values.
+struct Rows {
+    std::vector<uint8_t>  pay;
+    std::vector<uint16_t> sc;
+    std::vector<float>    deq;
+};
+
+Rows pack_rows(Fmt f, const std::vector<uint16_t>& x, size_t rows, int D, int G) {
+    Rows r;
+    const size_t n = rows * D;
+    r.deq.resize(n);
+    if (is_f16(f)) {
+        r.pay.resize(n * 2);
+        std::memcpy(r.pay.data(), x.data(), n * 2);
+        for (size_t i = 0; i < n; ++i) r.deq[i] = oracle::f16_to_f32(x[i]);
+        return r;
+    }
+    std::vector<float> xf(n);
+    for (size_t i = 0; i < n; ++i) xf[i] = oracle::f16_to_f32(x[i]);
+    oracle::Quantized z = oracle::quantize(xf.data(), rows, D, G, qbits(f));
+    for (size_t i = 0; i < n; ++i) r.deq[i] = (float)oracle::dequant(z, i, D, G, qbits(f));
+    r.pay = std::move(z.data);
+    r.sc = std::move(z.scale);
+    return r;
+}
+
+// Reference output of Hq query heads over Hkv heads of L rows ([Hkv][L][D]).
+std::vector<float> reference_gqa(const Rows& k, const Rows& v, const uint16_t* q, int Hq, int Hkv, int L, int D) {
+    std::vector<float> out((size_t)Hq * D, 0.f);
+    if (L == 0) return out;
+    for (int h = 0; h < Hq; ++h) {
+        const size_t off = (size_t)(h / (Hq / Hkv)) * L * D;
+        const std::vector<float> o = oracle::reference(k.deq.data() + off, v.deq.data() + off, q + (size_t)h * D, 1, L, D);
+        std::copy(o.begin(), o.end(), out.begin() + (size_t)h * D);
+    }
+    return out;
+}
+
+bool gate(const std::vector<uint16_t>& got, const std::vector<float>& ref, double* maxerr) {
+    bool ok = true;
+    *maxerr = 0.0;
+    for (size_t i = 0; i < got.size(); ++i) {
+        const double g = half_to_double(got[i]), r = (double)ref[i];
+        const double err = std::fabs(g - r);
+        if (!(err <= 3e-3 + 2e-2 * std::fabs(r))) ok = false;     // NaN fails too
+        *maxerr = std::max(*maxerr, std::isnan(err) ? INFINITY : err);
+    }
+    return ok;
+}
+
+bool gqa_case(Fmt f, int Hq, int Hkv, int L, int D, int G, int S, uint32_t seed, double* maxerr) {
+    const size_t n = (size_t)Hkv * L * D;
+    const Rows k = pack_rows(f, draw_f16(n, seed), (size_t)Hkv * L, D, G);
+    const Rows v = pack_rows(f, draw_f16(n, seed + 1), (size_t)Hkv * L, D, G);
+    const std::vector<uint16_t> q = draw_f16((size_t)Hq * D, seed + 2);
+    const std::vector<float> ref = reference_gqa(k, v, q.data(), Hq, Hkv, L, D);
+    if (S == 0) S = pick_splits_gqa(f, Hq, Hkv, L, D);
+    DeviceBuffer K(k.pay.size()), V(v.pay.size()), dq(q.size() * 2), out(q.size() * 2), ws(ws_bytes(Hq, D, S));
+    K.upload(k.pay.data(), k.pay.size());
+    V.upload(v.pay.data(), v.pay.size());
+    dq.upload(q.data(), q.size() * 2);
+    DeviceBuffer sK, sV;
+    DeviceBufs b{K.get(), V.get(), nullptr, nullptr, dq.as<uint16_t>(), out.as<uint16_t>(), ws.as<float>()};
+    if (!is_f16(f)) {
+        sK = DeviceBuffer(k.sc.size() * 2);
+        sV = DeviceBuffer(v.sc.size() * 2);
+        sK.upload(k.sc.data(), k.sc.size() * 2);
+        sV.upload(v.sc.data(), v.sc.size() * 2);
+        b.scK = sK.get();
+        b.scV = sV.get();
+    }
+    launch_gqa(f, b, Hq, Hkv, L, D, S, G);
+    check(va_sync());
+    std::vector<uint16_t> got(q.size());
+    out.download(got.data(), got.size() * 2);
+    return gate(got, ref, maxerr);
+}
+
+// A batch written into a page pool by two appends per sequence (rows
+// [0, len/2) then [len/2, len), the second at a non-zero start), checked
+// byte for byte against the host's packing, then decoded from the pool.
+bool paged_case(Fmt f, int Hq, int Hkv, int D, int G, int P, const std::vector<int>& lens, uint32_t seed,
+                double* maxerr, bool* pool_ok) {
+    const int B = (int)lens.size();
+    const bool quant = !is_f16(f);
+    const size_t rb = is_f16(f) ? (size_t)D * 2 : oracle::packed_bytes(qbits(f), D);
+    const int ng = D / G;
+    int max_pages = 1, num_pages = 2;                               // two pages nothing points at
+    for (int L : lens) { max_pages = std::max(max_pages, (L + P - 1) / P); num_pages += (L + P - 1) / P; }
+    // page ids: a seeded shuffle of the pool; unused table entries hold an invalid id
+    std::vector<int32_t> perm(num_pages);
+    for (int i = 0; i < num_pages; ++i) perm[i] = i;
+    oracle::Mt19937 g(seed);
+    for (int i = num_pages - 1; i > 0; --i) std::swap(perm[i], perm[g.next() % (uint32_t)(i + 1)]);
+    std::vector<int32_t> table((size_t)B * max_pages, -1);
+    for (int b = 0, at = 0; b < B; ++b)
+        for (int p = 0; p < (lens[b] + P - 1) / P; ++p) table[(size_t)b * max_pages + p] = perm[at++];
+
+    PagedShape sh{};
+    sh.B = B; sh.Hq = Hq; sh.Hkv = Hkv; sh.D = D; sh.G = G; sh.page_rows = P;
+    sh.max_pages = max_pages; sh.num_pages = num_pages;
+    sh.max_seq_len = std::max(1, *std::max_element(lens.begin(), lens.end()));
+
+    const size_t pool = page_bytes(f, Hkv, P, D) * num_pages;
+    const size_t spool = quant ? page_scale_bytes(f, Hkv, P, D, G) * num_pages : 0;
+    std::vector<uint8_t> kexp(pool, 0), vexp(pool, 0);
+    std::vector<uint16_t> ksexp(spool / 2, 0), vsexp(spool / 2, 0);
+    DeviceBuffer Kp(pool), Vp(pool), KS(std::max<size_t>(spool, 2)), VS(std::max<size_t>(spool, 2));
+    check(va_memset(Kp.get(), 0, pool));
+    check(va_memset(Vp.get(), 0, pool));
+    check(va_memset(KS.get(), 0, KS.bytes()));
+    check(va_memset(VS.get(), 0, VS.bytes()));
+    DeviceBuffer dtable(table.size() * 4), dlens((size_t)B * 4);
+    dtable.upload(table.data(), table.size() * 4);
+    dlens.upload(lens.data(), (size_t)B * 4);
+
+    const std::vector<uint16_t> q = draw_f16((size_t)B * Hq * D, seed + 3);
+    std::vector<float> ref((size_t)B * Hq * D, 0.f);
+    for (int b = 0; b < B; ++b) {
+        const int L = lens[b];
+        if (L == 0) continue;
+        const size_t n = (size_t)Hkv * L * D;
+        const std::vector<uint16_t> xk = draw_f16(n, seed + 10 * (uint32_t)b + 4);
+        const std::vector<uint16_t> xv = draw_f16(n, seed + 10 * (uint32_t)b + 5);
+        const Rows k = pack_rows(f, xk, (size_t)Hkv * L, D, G), v = pack_rows(f, xv, (size_t)Hkv * L, D, G);
+        const std::vector<float> r = reference_gqa(k, v, q.data() + (size_t)b * Hq * D, Hq, Hkv, L, D);
+        std::copy(r.begin(), r.end(), ref.begin() + (size_t)b * Hq * D);
+        // host packing of the pool: row j of head h -> page table[b][j / P], row j % P
+        for (int h = 0; h < Hkv; ++h)
+            for (int j = 0; j < L; ++j) {
+                const size_t page = (size_t)table[(size_t)b * max_pages + j / P];
+                const size_t dst = (page * Hkv + h) * P + (size_t)(j % P), src = (size_t)h * L + j;
+                std::memcpy(&kexp[dst * rb], &k.pay[src * rb], rb);
+                std::memcpy(&vexp[dst * rb], &v.pay[src * rb], rb);
+                if (quant) {
+                    std::memcpy(&ksexp[dst * ng], &k.sc[src * ng], (size_t)ng * 2);
+                    std::memcpy(&vsexp[dst * ng], &v.sc[src * ng], (size_t)ng * 2);
+                }
+            }
+        // two appends of this sequence alone (B = 1 over its block-table row)
+        PagedShape one = sh;
+        one.B = 1;
+        const int half = L / 2;
+        for (int part = 0; part < 2; ++part) {
+            const int r0 = part ? half : 0, nr = part ? L - half : half;
+            if (nr == 0) continue;
+            std::vector<uint16_t> xs((size_t)Hkv * nr * D), vs((size_t)Hkv * nr * D);
+            for (int h = 0; h < Hkv; ++h) {
+                std::memcpy(&xs[(size_t)h * nr * D], &xk[((size_t)h * L + r0) * D], (size_t)nr * D * 2);
+                std::memcpy(&vs[(size_t)h * nr * D], &xv[((size_t)h * L + r0) * D], (size_t)nr * D * 2);
+            }
+            DeviceBuffer dx(xs.size() * 2), dv(vs.size() * 2), dstart(4);
+            dx.upload(xs.data(), xs.size() * 2);
+            dv.upload(vs.data(), vs.size() * 2);
+            const int32_t st = r0;
+            dstart.upload(&st, 4);
+            const int32_t* trow = dtable.as<int32_t>() + (size_t)b * max_pages;
+            append_kv(f, dx.as<uint16_t>(), nr, dstart.as<int32_t>(), trow, one, Kp.get(), quant ? KS.as<uint16_t>() : nullptr);
+            append_kv(f, dv.as<uint16_t>(), nr, dstart.as<int32_t>(), trow, one, Vp.get(), quant ? VS.as<uint16_t>() : nullptr);
+            check(va_sync());
+        }
+    }
+    std::vector<uint8_t> kgot(pool), vgot(pool);
+    Kp.download(kgot.data(), pool);
+    Vp.download(vgot.data(), pool);
+    *pool_ok = kgot == kexp && vgot == vexp;
+    if (quant) {
+        std::vector<uint16_t> ksgot(spool / 2), vsgot(spool / 2);
+        KS.download(ksgot.data(), spool);
+        VS.download(vsgot.data(), spool);
+        *pool_ok = *pool_ok && ksgot == ksexp && vsgot == vsexp;
+    }
+
+    const int S = pick_splits_paged(f, sh);
+    DeviceBuffer dq(q.size() * 2), out(q.size() * 2), ws(ws_bytes(B * Hq, D, S));
+    dq.upload(q.data(), q.size() * 2);
+    PagedBufs pb;
+    pb.K = Kp.get(); pb.V = Vp.get();
+    if (quant) { pb.scK = KS.get(); pb.scV = VS.get(); }
+    pb.block_table = dtable.as<int32_t>();
+    pb.seq_lens = dlens.as<int32_t>();
+    pb.q = dq.as<uint16_t>();
+    pb.out = out.as<uint16_t>();
+    pb.ws = ws.as<float>();
+    launch_paged(f, pb, sh, S);
+    check(va_sync());
+    std::vector<uint16_t> got(q.size());
+    out.download(got.data(), got.size() * 2);
+    return gate(got, ref, maxerr);
+}
+
+int selftest_ex() {
+    const Fmt tiled[] = {Fmt::F16M, Fmt::Q8M, Fmt::Q4M, Fmt::Q3M};
+    struct GqaCase { int Hq, Hkv, L, D, S; };
+    const GqaCase gcases[] = {{8, 2, 1000, 128, 0}, {8, 2, 1000, 128, 3}, {12, 4, 777, 64, 0}, {6, 6, 513, 128, 2}};
+    int fails = 0, n = 0;
+    for (Fmt f : tiled)
+        for (int G : {32, 64}) {
+            if (is_f16(f) && G != 64) continue;
+            for (const GqaCase& c : gcases) {
+                double maxerr = 0.0;
+                const uint32_t seed = 0x5151u + (uint32_t)(c.Hq * 131 + c.L * 7 + c.D + c.S + G);
+                const bool ok = gqa_case(f, c.Hq, c.Hkv, c.L, c.D, G, c.S, seed, &maxerr);
+                std::printf("gqa    %-4s Hq=%-2d Hkv=%-2d L=%-5d D=%-3d S=%-2d G=%-2d  maxerr=%.2e  %s\n", fmt_name(f),
+                            c.Hq, c.Hkv, c.L, c.D, c.S, G, maxerr, ok ? "PASS" : "FAIL");
+                fails += !ok;
+                ++n;
+            }
+            for (int P : {64, 256}) {
+                double maxerr = 0.0;
+                bool pool_ok = false;
+                const std::vector<int> lens = {1, 300, 0, 777, 64};
+                const bool ok = paged_case(f, 8, 2, 128, G, P, lens, 0x77u + (uint32_t)(P + G), &maxerr, &pool_ok);
+                std::printf("paged  %-4s Hq=8  Hkv=2  P=%-3d lens=1,300,0,777,64 G=%-2d  maxerr=%.2e  append %s  %s\n",
+                            fmt_name(f), P, G, maxerr, pool_ok ? "bit-exact" : "MISMATCH", ok && pool_ok ? "PASS" : "FAIL");
+                fails += !(ok && pool_ok);
+                ++n;
+            }
+        }
+    if (fails) { std::printf("%d of %d grouped/paged case(s) FAILED\n", fails, n); return 1; }
+    std::printf("all %d grouped/paged cases passed\n", n);
     return 0;
 }
 
@@ -308,7 +548,7 @@ int main(int argc, char** argv) {
                 if (i + 1 >= argc) throw std::runtime_error("missing value for " + a);
                 return argv[++i];
             };
-            if (a == "--selftest" || a == "--bench" || a == "--probe") mode = a;
+            if (a == "--selftest" || a == "--selftest-ex" || a == "--bench" || a == "--probe") mode = a;
             else if (a == "--G") G = std::stoi(next());
             else if (a == "--reps") reps = std::max(1, std::stoi(next()));
             else if (a == "--set-gib") set_gib = std::stod(next());
@@ -322,6 +562,7 @@ int main(int argc, char** argv) {
             std::printf("measured read ceiling: %.1f GB/s\n", probe());
             return 0;
         }
+        if (mode == "--selftest-ex") return selftest_ex();
         const int rc = selftest();                             // --bench is gated on it (src/voltattn.cu:1075)
         if (rc || mode == "--selftest") return rc;
         std::printf("\n");

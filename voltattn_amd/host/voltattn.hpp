@@ -4,6 +4,14 @@
 //   voltattn::Fmt         enum class Fmt {F16, F16M, Q8, Q8M, Q4, Q4M, Q3M}  (src/voltattn.cu:676)
 //   voltattn::DeviceBufs  struct DeviceBufs {K, V, scK, scV, q, out, ws}      (src/voltattn.cu:796-801)
 //   voltattn::launch      launch(f, b, H, L, D, S) (+ group size G)           (src/voltattn.cu:803-835)
+//   voltattn::launch_splits / merge   the two passes of launch() on their own
+//                         (src/voltattn.cu:813-833 and combine, 651-672)
+//   voltattn::pick_splits the reference's split rule (src/voltattn.cu:1026)
+//   voltattn::quantize    device quantize() (src/voltattn.cu:705-745)
+//
+// Beyond the reference (its README.md:205-206 lists GQA and paged KV as
+// missing): launch_gqa, launch_paged, append_kv, and the Stream / Graph
+// helpers for replaying captured decode steps.
 //
 // Errors throw voltattn::Error (status code + message), where the reference
 // exits through CUDA_CHECK (src/voltattn.cu:49-58).
@@ -69,6 +77,94 @@ inline void launch(Fmt f, const DeviceBufs& b, int H, int L, int D, int S, int G
     check(va_decode(static_cast<va_fmt>(f), &cb, H, L, D, G, S, stream));
 }
 
+// The two passes of launch() on their own: partials into b.ws, then the merge.
+inline void launch_splits(Fmt f, const DeviceBufs& b, int H, int L, int D, int S, int G = 64,
+                          void* stream = nullptr) {
+    const va_bufs cb = to_c(b);
+    check(va_decode_splits(static_cast<va_fmt>(f), &cb, H, L, D, G, S, stream));
+}
+inline void merge(const float* ws, uint16_t* out, int H, int D, int S, void* stream = nullptr) {
+    check(va_merge(ws, out, H, D, S, stream));
+}
+
+inline size_t ws_bytes(int H, int D, int S) { return va_ws_bytes(H, D, S); }
+inline size_t payload_bytes(Fmt f, int H, int L, int D) {
+    return va_payload_bytes(static_cast<va_fmt>(f), H, L, D);
+}
+inline size_t scale_bytes(Fmt f, int H, int L, int D, int G = 64) {
+    return va_scale_bytes(static_cast<va_fmt>(f), H, L, D, G);
+}
+inline int pick_splits(Fmt f, int H, int L, int D) {
+    int S = 0;
+    check(va_pick_splits(static_cast<va_fmt>(f), H, L, D, &S));
+    return S;
+}
+
+// Grouped-query decode of one sequence: Hq query heads over Hkv KV heads
+// (query head i reads KV head i / (Hq / Hkv)); b.q and b.out are [Hq][D],
+// b.ws holds ws_bytes(Hq, D, S). S = 0 picks the split count.
+inline void launch_gqa(Fmt f, const DeviceBufs& b, int Hq, int Hkv, int L, int D, int S = 0,
+                       int G = 64, void* stream = nullptr) {
+    const va_bufs cb = to_c(b);
+    check(va_decode_gqa(static_cast<va_fmt>(f), &cb, Hq, Hkv, L, D, G, S, stream));
+}
+inline int pick_splits_gqa(Fmt f, int Hq, int Hkv, int L, int D) {
+    int S = 0;
+    check(va_pick_splits_gqa(static_cast<va_fmt>(f), Hq, Hkv, L, D, &S));
+    return S;
+}
+
+// A batch decoded from a page pool (va_paged_shape documents the layout).
+using PagedShape = va_paged_shape;
+
+struct PagedBufs {
+    void*          K           = nullptr;   // K page pool
+    void*          V           = nullptr;   // V page pool
+    void*          scK         = nullptr;   // K scale pool (quantized formats)
+    void*          scV         = nullptr;   // V scale pool
+    const int32_t* block_table = nullptr;   // [B][max_pages]
+    const int32_t* seq_lens    = nullptr;   // [B]
+    uint16_t*      q           = nullptr;   // [B][Hq][D]
+    uint16_t*      out         = nullptr;   // [B][Hq][D]
+    float*         ws          = nullptr;   // ws_bytes(B * Hq, D, S)
+};
+
+inline va_paged_bufs to_c(const PagedBufs& b) {
+    return va_paged_bufs{b.K, b.V, static_cast<const uint16_t*>(b.scK), static_cast<const uint16_t*>(b.scV),
+                         b.block_table, b.seq_lens, b.q, b.out, b.ws};
+}
+
+inline void launch_paged(Fmt f, const PagedBufs& b, const PagedShape& shape, int S = 0,
+                         void* stream = nullptr) {
+    const va_paged_bufs cb = to_c(b);
+    check(va_decode_paged(static_cast<va_fmt>(f), &cb, &shape, S, stream));
+}
+inline int pick_splits_paged(Fmt f, const PagedShape& shape) {
+    int S = 0;
+    check(va_pick_splits_paged(static_cast<va_fmt>(f), &shape, &S));
+    return S;
+}
+inline size_t page_bytes(Fmt f, int Hkv, int page_rows, int D) {
+    return va_page_bytes(static_cast<va_fmt>(f), Hkv, page_rows, D);
+}
+inline size_t page_scale_bytes(Fmt f, int Hkv, int page_rows, int D, int G = 64) {
+    return va_page_scale_bytes(static_cast<va_fmt>(f), Hkv, page_rows, D, G);
+}
+
+// The cache write path: quantize (or copy, f16 formats) n fp16 rows per
+// (sequence, KV head) of x [B][Hkv][n][D] into the page pool at positions
+// start[b] .. start[b] + n - 1.
+inline void append_kv(Fmt f, const uint16_t* x, int n, const int32_t* start, const int32_t* block_table,
+                      const PagedShape& shape, void* pages, uint16_t* scales, void* stream = nullptr) {
+    check(va_append_kv(static_cast<va_fmt>(f), x, n, start, block_table, &shape, pages, scales, stream));
+}
+
+// Device quantize() of fp32 rows [rows][D] into packed codes and fp16 scales.
+inline void quantize(int bits, int G, const float* x, size_t rows, int D, void* packed, uint16_t* scales,
+                     void* stream = nullptr) {
+    check(va_quantize(bits, G, x, rows, D, packed, scales, stream));
+}
+
 // RAII device allocation.
 class DeviceBuffer {
 public:
@@ -113,6 +209,38 @@ public:
     }
 private:
     void* e_ = nullptr;
+};
+
+// RAII stream at the default priority.
+class Stream {
+public:
+    Stream() { check(va_stream_create(&s_)); }
+    ~Stream() { if (s_) (void)va_stream_destroy(s_); }
+    Stream(const Stream&) = delete;
+    Stream& operator=(const Stream&) = delete;
+    void* get() const { return s_; }
+    void sync() { check(va_stream_sync(s_)); }
+private:
+    void* s_ = nullptr;
+};
+
+// A captured launch sequence, replayed with launch(): begin(stream), the
+// launches on that stream, end().
+class Graph {
+public:
+    Graph() = default;
+    ~Graph() { if (g_) (void)va_graph_destroy(g_); }
+    Graph(const Graph&) = delete;
+    Graph& operator=(const Graph&) = delete;
+    void begin(void* stream) { check(va_graph_begin(stream)); s_ = stream; }
+    void end() {
+        if (g_) { (void)va_graph_destroy(g_); g_ = nullptr; }
+        check(va_graph_end(s_, &g_));
+    }
+    void launch(void* stream) const { check(va_graph_launch(g_, stream)); }
+private:
+    void* g_ = nullptr;
+    void* s_ = nullptr;
 };
 
 } // namespace voltattn
