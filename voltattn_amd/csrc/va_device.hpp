@@ -146,21 +146,50 @@ __device__ __forceinline__ float lane_xor32(float x) {
     return __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute(src, __builtin_bit_cast(int, x)));
 }
 
+// x combined over the four 16-lane rows (lanes l, l^16, l^32, l^48), in
+// every lane, with gfx950's v_permlane16_swap / v_permlane32_swap (VALU, no LDS
+// round trip). With both operands holding v, permlane16_swap leaves rows
+// {v0, v0, v2, v2} and {v1, v1, v3, v3}, permlane32_swap halves {lo, lo} and
+// {hi, hi} (probed on MI355X). Every lane gets (v0 (+) v1) (+) (v2 (+) v3), bit
+// for bit the same. The swaps are written as inline asm on two read-write
+// operands: this compiler's builtins lose the second result when both results
+// feed one instruction. The s_nop before covers the VALU-write -> permlane-read
+// wait states the compiler inserts for the builtin; the one after is spare.
+__device__ __forceinline__ void permlane16_swap(unsigned& a, unsigned& b) {
+    asm volatile("s_nop 1\n\tv_permlane16_swap_b32 %0, %1\n\ts_nop 1" : "+v"(a), "+v"(b));
+}
+__device__ __forceinline__ void permlane32_swap(unsigned& a, unsigned& b) {
+    asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1\n\ts_nop 1" : "+v"(a), "+v"(b));
+}
+__device__ __forceinline__ float rows_sum(float x) {
+    unsigned a = __builtin_bit_cast(unsigned, x), b = a;
+    permlane16_swap(a, b);
+    x = __builtin_bit_cast(float, a) + __builtin_bit_cast(float, b);
+    a = __builtin_bit_cast(unsigned, x);
+    b = a;
+    permlane32_swap(a, b);
+    return __builtin_bit_cast(float, a) + __builtin_bit_cast(float, b);
+}
+__device__ __forceinline__ float rows_max(float x) {
+    unsigned a = __builtin_bit_cast(unsigned, x), b = a;
+    permlane16_swap(a, b);
+    x = fmaxf(__builtin_bit_cast(float, a), __builtin_bit_cast(float, b));
+    a = __builtin_bit_cast(unsigned, x);
+    b = a;
+    permlane32_swap(a, b);
+    return fmaxf(__builtin_bit_cast(float, a), __builtin_bit_cast(float, b));
+}
+
 // Full-wave max and sum (all 64 lanes receive the result).
 __device__ __forceinline__ float wave_max(float x) {
     x = fmaxf(x, dpp<DPP_QP_XOR1>(x));
     x = fmaxf(x, dpp<DPP_QP_XOR2>(x));
     x = fmaxf(x, dpp<DPP_ROW_HALF_MIRROR>(x));
     x = fmaxf(x, dpp<DPP_ROW_MIRROR>(x));
-    x = fmaxf(x, swz_xor<16>(x));
-    x = fmaxf(x, lane_xor32(x));
-    return x;
+    return rows_max(x);
 }
 __device__ __forceinline__ float wave_sum(float x) {
-    x = group_sum<16>(x);
-    x += swz_xor<16>(x);
-    x += lane_xor32(x);
-    return x;
+    return rows_sum(group_sum<16>(x));
 }
 
 } // namespace va

@@ -259,8 +259,7 @@ __global__ __launch_bounds__(WAVES * 64, 1) void decode_mfma(DecodeArgs a) {
                     lmax = fmaxf(lmax, fabsf(qe[8 * i + e]));
                 }
             }
-            float cmax = fmaxf(lmax, swz_xor<16>(lmax));
-            cmax = fmaxf(cmax, lane_xor32(cmax));       // column maximum over the quarters
+            const float cmax = rows_max(lmax);          // column maximum over the quarters
             int sh = 0;
             if (cmax > 0.f) sh = 22 - ((int)((__builtin_bit_cast(uint32_t, cmax) >> 23) & 0xFF) - 126);
             const float up = __builtin_bit_cast(float, (uint32_t)(127 + sh) << 23);
@@ -292,8 +291,7 @@ __global__ __launch_bounds__(WAVES * 64, 1) void decode_mfma(DecodeArgs a) {
             if constexpr (Q4) {                   // codes enter as n = v + 8
 #pragma unroll
                 for (int k = 0; k < 3; ++k) {
-                    float cs = dsum[k] + swz_xor<16>(dsum[k]);
-                    cs += lane_xor32(cs);
+                    const float cs = rows_sum(dsum[k]);
                     qoff[k] = -8 * (int)cs;
                 }
             }
@@ -403,8 +401,7 @@ __global__ __launch_bounds__(WAVES * 64, 1) void decode_mfma(DecodeArgs a) {
                 float mx = fmaxf(mq, tmax);
                 if constexpr (NG == 4) { mx = fmaxf(mx, dpp<dpp_row_ror(8)>(mx)); mx = fmaxf(mx, dpp<dpp_row_ror(4)>(mx)); }
                 if constexpr (NG == 2) { mx = fmaxf(mx, dpp<dpp_row_ror(8)>(mx)); }
-                mx = fmaxf(mx, swz_xor<16>(mx));
-                mx = fmaxf(mx, lane_xor32(mx));
+                mx = rows_max(mx);
                 const float c = fast_exp2(mq - mx);
                 mq = mx;
                 lsum *= c;
@@ -424,8 +421,7 @@ __global__ __launch_bounds__(WAVES * 64, 1) void decode_mfma(DecodeArgs a) {
             // Row exponent: keep operands <= 2^15 (fp16 range), and after a new
             // maximum re-centre them near 2^14 so the lo halves stay normal.
             if (raise || __builtin_amdgcn_ballot_w64(xmax > 32768.f)) {
-                float mc = fmaxf(xmax, swz_xor<16>(xmax));
-                mc = fmaxf(mc, lane_xor32(mc));                 // max of the row (column) over quarters
+                const float mc = rows_max(xmax);                // max of the row (column) over quarters
                 int dl = 0;
                 if (mc > 0.f) dl = 14 - ((int)((__builtin_bit_cast(uint32_t, mc) >> 23) & 0xFF) - 126);
                 dl = max(-100 - (int)ex, min(100 - (int)ex, dl));
@@ -467,8 +463,7 @@ __global__ __launch_bounds__(WAVES * 64, 1) void decode_mfma(DecodeArgs a) {
     // ---- work-group merge. Per query slot q: lsum of column q summed over the
     // 4 quarters (every group column of q holds the same sum), m = mq; o row
     // (cg', q) drops its row factor 2^ex (an exact power of two).
-    float lt = lsum + swz_xor<16>(lsum);
-    lt += lane_xor32(lt);
+    const float lt = rows_sum(lsum);
     if (lane < QG) {
         s_l[lane][wave] = lt;
         s_m[lane][wave] = mq;
