@@ -15,6 +15,9 @@ namespace va {
 // the code object; layout in va_kernels.hpp).
 static __device__ __align__(256) unsigned g_tickets[TICKET_SLOTS * TICKET_MAXH * TICKET_STRIDE];
 static __device__ __align__(256) uint64_t g_parts[(size_t)TICKET_SLOTS * PART_CAP * PART_STRIDE];
+// Plain fp32 partials of the counted protocol (their own store, so a stale
+// word of one protocol is never read by the other).
+static __device__ __align__(256) float g_partf[(size_t)TICKET_SLOTS * PART_CAP * PARTF_STRIDE];
 
 constexpr int POLL_MAX = 1 << 12;   // bound on re-reads of one in-flight word
 
@@ -52,7 +55,15 @@ struct Route {
 //
 // Two-pass form (ticket_slot < 0): the partials go to ws[(oh0+q)*S + s].
 //
-// Fused form: every value of a partial is stored as one 64-bit word
+// Fused form, two protocols (measured on MI355X): with one query slot per
+// work-group the partials are tagged, so the merging work-group never waits
+// for another group's stores to complete (finish_tagged); with several slots
+// the merge reads QG*S partials and its bytes dominate, so the partials are
+// plain fp32 (half the bytes) behind a count of completed stores
+// (finish_counted): 0.9-1.8 us less per grouped step at Hq 32 / Hkv 8,
+// L 65536, and 0.1-0.4 us more per one-slot step.
+
+// Tagged protocol: every value of a partial is stored as one 64-bit word
 // (tag << 32 | fp32 bits), tag = (epoch << 11 | mg << 1 | 1), unique per merge
 // group and call and never zero; a partial is PART_STRIDE words: m, l,
 // o[0..D), and partial (q, s) of merge group mg sits at (mg*QG + q)*S + s.
@@ -74,28 +85,13 @@ struct Route {
 // (no positions) gives a zero output; a non-finite one (an invalid input that
 // the kernel flagged with l = NaN) gives NaN. Needs S <= 64.
 template <int D, int NT, int QG>
-__device__ void finish_partial(const DecodeArgs& a, const Route& rt, const float (&M)[QG],
-                               const float (&ls)[QG], const float (&acc)[QG], unsigned epoch) {
+__device__ void finish_tagged(const DecodeArgs& a, const Route& rt, const float (&M)[QG],
+                              const float (&ls)[QG], const float (&acc)[QG], unsigned epoch) {
     constexpr int NW = NT / 64;
     constexpr uint32_t PB = PART_STRIDE * 8;    // bytes per partial (16-byte multiple)
     static_assert(PB % 16 == 0 && D + 2 <= PART_STRIDE, "partial layout");
     const int t = (int)threadIdx.x;
     const int S = a.S, s = rt.s;
-    if (a.ticket_slot < 0) {
-        if (t < D) {
-#pragma unroll
-            for (int q = 0; q < QG; ++q) {
-                if (q >= rt.nq) break;
-                float* slot = a.ws + ((size_t)(rt.oh0 + q) * S + s) * (D + 2);
-                store_dev(slot + 2 + t, acc[q]);
-                if (t == 0) {
-                    store_dev(slot, M[q]);
-                    store_dev(slot + 1, ls[q]);
-                }
-            }
-        }
-        return;
-    }
     // The merge splits the NW waves over the query slots: WQ = NW / QG waves per
     // slot (all waves on one slot when QG = 1); wave w merges slot w / WQ and
     // folds its splits j = sw, sw + WQ, ... (sw = w % WQ) in increasing order.
@@ -242,6 +238,189 @@ __device__ void finish_partial(const DecodeArgs& a, const Route& rt, const float
         store_dev(ticket, 0u);
         store_dev(ticket + 1, epoch + 1u);
     }
+}
+
+// Counted protocol: thread NT-1 takes the merge group's ticket first (word 0 of the
+// group's ticket line). A work-group that does not complete the ticket stores
+// its partials as plain fp32 (o[0..D), m, l; PSF floats each, partial (q, s) of
+// merge group mg at (mg*QG + q)*S + s) with device-coherent stores, waits
+// until they have completed (every thread, then the barrier) and counts itself
+// in word 2 of the line. The work-group that completes the ticket keeps its own
+// partials in LDS, waits (bounded) until the other S-1 have counted, and
+// merges: it waits only for groups that have already taken their ticket, so
+// every wait ends.
+//
+// The merge spreads the loads over all NT/64 waves and runs the query slots
+// side by side: WQ = NW/QG waves per slot; lane j of each of them reads split
+// j's (m, l), and sub-wave sw folds splits j = sw, sw + WQ, ... in increasing
+// order into 4-dimension columns with split j's weight read by readlane; the
+// WQ sub-wave sums are added in order through LDS. The order is fixed, so the
+// result does not depend on arrival order. A merged l of zero (no positions)
+// gives a zero output; a non-finite one (an invalid input that the kernel
+// flagged with l = NaN) gives NaN, and so does a count that never completes
+// within the poll bound. Needs S <= 64.
+template <int D, int NT, int QG>
+__device__ void finish_counted(const DecodeArgs& a, const Route& rt, const float (&M)[QG],
+                               const float (&ls)[QG], const float (&acc)[QG]) {
+    constexpr int NW = NT / 64;
+    constexpr int PSF = D + 4;                   // floats per partial: o[D], m, l, 2 spare (16-byte rows)
+    constexpr uint32_t PB = PSF * 4;
+    static_assert(PSF <= PARTF_STRIDE, "partial store");
+    const int t = (int)threadIdx.x;
+    const int S = a.S, s = rt.s;
+    constexpr int WQ = NW / QG;
+    static_assert(NW >= QG && NW % QG == 0, "whole waves per query slot");
+    constexpr int RB = QG > 1 ? 16 : 4;          // o loads per wave per batch
+    __shared__ int   s_last, s_bad;
+    __shared__ float s_own[QG][D + 2];
+    __shared__ float s_fold[QG][WQ][D];
+    __shared__ float s_lsum[QG];
+    unsigned* line = g_tickets + ((size_t)a.ticket_slot * TICKET_MAXH + rt.mg) * TICKET_STRIDE;
+    if (t == NT - 1)
+        s_last = __hip_atomic_fetch_add(line, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+                 (unsigned)(S - 1);
+    __syncthreads();
+    float* base = g_partf + (size_t)a.ticket_slot * PART_CAP * PARTF_STRIDE + (size_t)rt.mg * QG * S * PSF;
+    if (!s_last) {
+        if (t < D) {
+#pragma unroll
+            for (int q = 0; q < QG; ++q) {
+                if (q >= rt.nq) break;
+                float* mine = base + ((size_t)q * S + s) * PSF;
+                store_dev(mine + t, acc[q]);
+                if (t == 0) {
+                    store_dev(mine + D, M[q]);
+                    store_dev(mine + D + 1, ls[q]);
+                }
+            }
+        }
+        // The stores are written through to the device coherence point (sc1):
+        // once each thread has seen its own complete, the count may go up.
+        wait_all_mem();
+        __syncthreads();
+        if (t == 0) __hip_atomic_fetch_add(line + 2, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        return;
+    }
+    if (t < D) {
+#pragma unroll
+        for (int q = 0; q < QG; ++q) {
+            if (q >= rt.nq) break;
+            s_own[q][t] = acc[q];
+            if (t == 0) {
+                s_own[q][D] = M[q];
+                s_own[q][D + 1] = ls[q];
+            }
+        }
+    }
+    if (t == 0) {                                // the other S - 1 partials stored?
+        unsigned n = load_dev(line + 2);
+        for (int k = 0; k < POLL_MAX && n < (unsigned)(S - 1); ++k) {
+            __builtin_amdgcn_s_sleep(2);
+            n = load_dev(line + 2);
+        }
+        s_bad = n < (unsigned)(S - 1);
+    }
+    __syncthreads();                             // the partial loads below are served from the coherence point (sc1)
+
+    const int w    = uniform(t >> 6);
+    const int lane = t & 63;
+    const int qw   = w / WQ, sw = w - (w / WQ) * WQ;
+    const int dq   = min(lane, D / 4 - 1);       // o quad of this lane: dims 4dq .. 4dq + 3
+    const int jl   = min(lane, S - 1);
+    const bool in_s = lane < S, own = lane == s;
+    if (qw < rt.nq) {                            // wave-uniform
+        const __amdgpu_buffer_rsrc_t rp = make_rsrc(base + (size_t)qw * S * PSF, (uint32_t)S * PB);
+        const int nsw = (S - sw + WQ - 1) / WQ;  // splits folded by this wave
+        // The words are taken out of each 16-byte vector right after its load
+        // (an array of the vectors carried across the loop is mis-compiled).
+        uint32_t op[RB][4];
+        auto load_batch = [&](int b0) {
+#pragma unroll
+            for (int i = 0; i < RB; ++i) {
+                const int j = sw + WQ * (b0 + i);
+                if (b0 + i < nsw) {
+                    const u32x4 x = ld128_dev(rp, (uint32_t)j * PB + (uint32_t)dq * 16u);
+                    op[i][0] = x.x; op[i][1] = x.y; op[i][2] = x.z; op[i][3] = x.w;
+                }
+            }
+        };
+        const uint32_t mlv = __builtin_amdgcn_raw_buffer_load_b32(rp, (uint32_t)jl * PB + D * 4, 0, 16);
+        const uint32_t llv = __builtin_amdgcn_raw_buffer_load_b32(rp, (uint32_t)jl * PB + D * 4 + 4, 0, 16);
+        load_batch(0);
+        asm volatile("" ::: "memory");
+        const float own_m = s_own[qw][D], own_l = s_own[qw][D + 1];
+        const float mj = !in_s ? -__builtin_inff() : own ? own_m : __builtin_bit_cast(float, mlv);
+        const float lj = !in_s ? 0.f : own ? own_l : __builtin_bit_cast(float, llv);
+        const float mx = wave_max(mj);
+        const float wj = fast_exp2(mj - mx);    // weight of split `lane` (0 past S)
+        const float lsum = wave_sum(wj * lj);
+        float o4[4] = {0.f, 0.f, 0.f, 0.f};
+        for (int b0 = 0; b0 < nsw; b0 += RB) {
+            if (b0 != 0) load_batch(b0);
+#pragma unroll
+            for (int i = 0; i < RB; ++i) {
+                if (b0 + i >= nsw) break;        // wave-uniform
+                const int j = sw + WQ * (b0 + i);
+                float v[4];
+                if (j == s) {                    // wave-uniform
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) v[e] = s_own[qw][4 * dq + e];
+                } else {
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) v[e] = __builtin_bit_cast(float, op[i][e]);
+                }
+                const float f = __builtin_bit_cast(float,
+                    __builtin_amdgcn_readlane(__builtin_bit_cast(int, wj), j));
+#pragma unroll
+                for (int e = 0; e < 4; ++e) o4[e] = __builtin_fmaf(f, v[e], o4[e]);
+            }
+        }
+        if (lane < D / 4) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) s_fold[qw][sw][4 * lane + e] = o4[e];
+        }
+        if (sw == 0 && lane == 0) s_lsum[qw] = lsum;
+    }
+    __syncthreads();
+    if (t < D) {
+#pragma unroll
+        for (int q = 0; q < QG; ++q) {
+            if (q >= rt.nq) break;
+            float o = 0.f;
+#pragma unroll
+            for (int v = 0; v < WQ; ++v) o += s_fold[q][v][t];
+            const float r = s_lsum[q] == 0.f ? 0.f : o / s_lsum[q];
+            a.out[(size_t)(rt.oh0 + q) * D + t] = s_bad ? (uint16_t)0x7E00u : f2h_rne(r);
+        }
+    }
+    if (t == 0) {                                // every partial is in: reset for the slot's next call
+        store_dev(line, 0u);
+        store_dev(line + 2, 0u);
+    }
+}
+
+template <int D, int NT, int QG>
+__device__ void finish_partial(const DecodeArgs& a, const Route& rt, const float (&M)[QG],
+                               const float (&ls)[QG], const float (&acc)[QG], unsigned epoch) {
+    const int t = (int)threadIdx.x;
+    const int S = a.S, s = rt.s;
+    if (a.ticket_slot < 0) {
+        if (t < D) {
+#pragma unroll
+            for (int q = 0; q < QG; ++q) {
+                if (q >= rt.nq) break;
+                float* slot = a.ws + ((size_t)(rt.oh0 + q) * S + s) * (D + 2);
+                store_dev(slot + 2 + t, acc[q]);
+                if (t == 0) {
+                    store_dev(slot, M[q]);
+                    store_dev(slot + 1, ls[q]);
+                }
+            }
+        }
+        return;
+    }
+    if constexpr (QG == 1) finish_tagged<D, NT, QG>(a, rt, M, ls, acc, epoch);
+    else finish_counted<D, NT, QG>(a, rt, M, ls, acc);
 }
 
 } // namespace va

@@ -36,12 +36,14 @@ struct DecodeArgs {
 
 // Fused second pass: per-(slot, merge group) ticket lines in static device
 // memory (zero at load): word 0 counts the arrivals of the group's
-// work-groups, word 1 is the group's call epoch, advanced by the merging
-// work-group. Calls rotate over TICKET_SLOTS slots, so up to that many decode
-// calls may be in flight on one device at once. Each line is 256 bytes: atomics
-// to one line serialize at the memory side, and the S arrivals of every group
-// land together. The partials of a fused call live in library memory (PART_CAP
-// partials of PART_STRIDE 64-bit words per slot), not in the caller's ws.
+// work-groups, word 1 is the group's call epoch (tagged protocol), advanced by
+// the merging work-group, word 2 counts the groups whose partials are stored
+// (counted protocol). Calls rotate over TICKET_SLOTS slots, so up to that many
+// decode calls may be in flight on one device at once. Each line is 256 bytes:
+// atomics to one line serialize at the memory side, and the S arrivals of every
+// group land together. The partials of a fused call live in library memory
+// (PART_CAP partials per slot: PART_STRIDE 64-bit words tagged, PARTF_STRIDE
+// floats plain), not in the caller's ws.
 // Calls with more than TICKET_MAXH merge groups, more than PART_CAP partials or
 // more than 64 splits use the two-pass form.
 constexpr int TICKET_SLOTS  = 16;
@@ -49,6 +51,7 @@ constexpr int TICKET_MAXH   = 1024;
 constexpr int TICKET_STRIDE = 64;   // uint32 per ticket line (256 bytes)
 constexpr int PART_CAP      = 2048; // partials (merge groups x QG x S) per slot
 constexpr int PART_STRIDE   = 130;  // 64-bit words per partial: m, l, o[D], D <= 128
+constexpr int PARTF_STRIDE  = 132;  // floats per plain partial: o[D], m, l (16-byte rows), D <= 128
 
 // Page ids of one split of the paged kernels are staged in LDS: a split may
 // span at most this many pages.
