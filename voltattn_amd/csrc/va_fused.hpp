@@ -252,10 +252,12 @@ __device__ void finish_tagged(const DecodeArgs& a, const Route& rt, const float 
 //
 // The merge spreads the loads over all NT/64 waves and runs the query slots
 // side by side: WQ = NW/QG waves per slot; lane j of each of them reads split
-// j's (m, l), and sub-wave sw folds splits j = sw, sw + WQ, ... in increasing
-// order into 4-dimension columns with split j's weight read by readlane; the
-// WQ sub-wave sums are added in order through LDS. The order is fixed, so the
-// result does not depend on arrival order. A merged l of zero (no positions)
+// j's (m, l), and sub-wave sw folds splits j = sw, sw + WQ, ... into
+// 4-dimension columns. Each 16-byte load instruction carries SPL = 256/D
+// splits (one per D/4-lane block), each block weighted by its split's weight
+// (readlane); the blocks are summed at the end by lane swaps, the WQ sub-wave
+// sums in order through LDS. The order is fixed, so the result does not depend
+// on arrival order. A merged l of zero (no positions)
 // gives a zero output; a non-finite one (an invalid input that the kernel
 // flagged with l = NaN) gives NaN, and so does a count that never completes
 // within the poll bound. Needs S <= 64.
@@ -270,7 +272,6 @@ __device__ void finish_counted(const DecodeArgs& a, const Route& rt, const float
     const int S = a.S, s = rt.s;
     constexpr int WQ = NW / QG;
     static_assert(NW >= QG && NW % QG == 0, "whole waves per query slot");
-    constexpr int RB = QG > 1 ? 16 : 4;          // o loads per wave per batch
     __shared__ int   s_last, s_bad;
     __shared__ float s_own[QG][D + 2];
     __shared__ float s_fold[QG][WQ][D];
@@ -325,20 +326,26 @@ __device__ void finish_counted(const DecodeArgs& a, const Route& rt, const float
     const int w    = uniform(t >> 6);
     const int lane = t & 63;
     const int qw   = w / WQ, sw = w - (w / WQ) * WQ;
-    const int dq   = min(lane, D / 4 - 1);       // o quad of this lane: dims 4dq .. 4dq + 3
-    const int jl   = min(lane, S - 1);
+    // Each load instruction carries SPL splits: lane = sub * NQD + dq reads the
+    // 4 dimensions 4dq .. 4dq + 3 of split sw + WQ * (SPL * i + sub).
+    constexpr int NQD = D / 4, SPL = 64 / NQD;
+    constexpr int RI  = QG > 1 ? 8 : 2;          // load instructions per wave per batch
+    const int dq  = lane % NQD, sub = lane / NQD;
+    const int jl  = min(lane, S - 1);
     const bool in_s = lane < S, own = lane == s;
     if (qw < rt.nq) {                            // wave-uniform
         const __amdgpu_buffer_rsrc_t rp = make_rsrc(base + (size_t)qw * S * PSF, (uint32_t)S * PB);
         const int nsw = (S - sw + WQ - 1) / WQ;  // splits folded by this wave
+        const int ni  = (nsw + SPL - 1) / SPL;   // load instructions
         // The words are taken out of each 16-byte vector right after its load
         // (an array of the vectors carried across the loop is mis-compiled).
-        uint32_t op[RB][4];
+        uint32_t op[RI][4];
         auto load_batch = [&](int b0) {
 #pragma unroll
-            for (int i = 0; i < RB; ++i) {
-                const int j = sw + WQ * (b0 + i);
-                if (b0 + i < nsw) {
+            for (int i = 0; i < RI; ++i) {
+                if (b0 + i < ni) {               // wave-uniform
+                    const int k = SPL * (b0 + i) + sub;
+                    const int j = sw + WQ * min(k, nsw - 1);   // lanes past the last split reread it (weight 0)
                     const u32x4 x = ld128_dev(rp, (uint32_t)j * PB + (uint32_t)dq * 16u);
                     op[i][0] = x.x; op[i][1] = x.y; op[i][2] = x.z; op[i][3] = x.w;
                 }
@@ -355,27 +362,49 @@ __device__ void finish_counted(const DecodeArgs& a, const Route& rt, const float
         const float wj = fast_exp2(mj - mx);    // weight of split `lane` (0 past S)
         const float lsum = wave_sum(wj * lj);
         float o4[4] = {0.f, 0.f, 0.f, 0.f};
-        for (int b0 = 0; b0 < nsw; b0 += RB) {
+        for (int b0 = 0; b0 < ni; b0 += RI) {
             if (b0 != 0) load_batch(b0);
 #pragma unroll
-            for (int i = 0; i < RB; ++i) {
-                if (b0 + i >= nsw) break;        // wave-uniform
-                const int j = sw + WQ * (b0 + i);
-                float v[4];
-                if (j == s) {                    // wave-uniform
+            for (int i = 0; i < RI; ++i) {
+                if (b0 + i >= ni) break;         // wave-uniform
+                // weight of this lane's split: readlane per sub-block, then select
+                float f = 0.f;
+                bool mine = false;
 #pragma unroll
-                    for (int e = 0; e < 4; ++e) v[e] = s_own[qw][4 * dq + e];
-                } else {
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) v[e] = __builtin_bit_cast(float, op[i][e]);
+                for (int r = 0; r < SPL; ++r) {
+                    const int k = SPL * (b0 + i) + r;
+                    const int j = sw + WQ * min(k, nsw - 1);
+                    const float fr = k < nsw ? __builtin_bit_cast(float,
+                        __builtin_amdgcn_readlane(__builtin_bit_cast(int, wj), j)) : 0.f;
+                    f = sub == r ? fr : f;
+                    mine = sub == r ? (k < nsw && j == s) : mine;
                 }
-                const float f = __builtin_bit_cast(float,
-                    __builtin_amdgcn_readlane(__builtin_bit_cast(int, wj), j));
+                float v[4];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) v[e] = __builtin_bit_cast(float, op[i][e]);
+                if (__builtin_amdgcn_ballot_w64(mine) != 0) {   // this group's own split: from LDS
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        const float ov = s_own[qw][4 * dq + e];
+                        v[e] = mine ? ov : v[e];
+                    }
+                }
 #pragma unroll
                 for (int e = 0; e < 4; ++e) o4[e] = __builtin_fmaf(f, v[e], o4[e]);
             }
         }
-        if (lane < D / 4) {
+        // sub-block sums in a fixed order: (s0 + s1) for SPL = 2, rows_sum for SPL = 4
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            if constexpr (SPL == 4) {
+                o4[e] = rows_sum(o4[e]);
+            } else {
+                unsigned x = __builtin_bit_cast(unsigned, o4[e]), y = x;
+                permlane32_swap(x, y);
+                o4[e] = __builtin_bit_cast(float, x) + __builtin_bit_cast(float, y);
+            }
+        }
+        if (lane < NQD) {
 #pragma unroll
             for (int e = 0; e < 4; ++e) s_fold[qw][sw][4 * lane + e] = o4[e];
         }
