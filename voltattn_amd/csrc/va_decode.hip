@@ -125,7 +125,7 @@ static TiledCfg default_cfg(int kind) {
         case KF16: return {8, false};    // 8 waves x 4 rows
         case KQ8:  return {4, true};     // 4 waves x 4 rows
         case KQ4:  return {4, true};     // 4 waves x 4 rows
-        default:   return {4, false};    // q3: 4 waves x 2 rows, two groups per CU
+        default:   return {8, false};    // q3: 8 waves x 2 rows (128 VGPRs: two waves per SIMD)
     }
 }
 
