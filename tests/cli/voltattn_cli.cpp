@@ -484,22 +484,35 @@ int bench(int G, const std::vector<int>& Ls, const std::vector<Fmt>& fmts, int r
     std::printf("| fmt  | L      | G  | S   | KV bytes  | best ms | mean ms | GB/s   | MBU   | %%8TB/s | tok/s  | vs f16 | vs f16+ |\n");
     std::printf("|------|--------|----|-----|-----------|---------|---------|--------|-------|--------|--------|--------|---------|\n");
     std::vector<Row> rows;
+    // Rows of one L are printed once all its formats are measured, so the
+    // vs-f16 / vs-f16+ ratios exist for every row ("-" where that format is
+    // not run at this L).
+    auto ratio = [](double base_ms, double ms) {
+        char buf[16];
+        if (base_ms > 0) std::snprintf(buf, sizeof buf, "%5.2fx", base_ms / ms);
+        else std::snprintf(buf, sizeof buf, "%6s", "-");
+        return std::string(buf);
+    };
     for (int L : Ls) {
         double f16_ms = 0, f16p_ms = 0;
+        std::vector<Row> block;
         for (Fmt f : fmts) {
             if (f == Fmt::Q3M || L <= 65536) {
                 const Row r = bench_one(f, H, L, D, G, reps, set_gib * 1073741824.0, stream);
                 if (f == Fmt::F16) f16_ms = r.best_ms;
                 if (f == Fmt::F16M) f16p_ms = r.best_ms;
-                const double gbs = r.bytes / (r.best_ms * 1e6);
-                std::printf("| %-4s | %-6d | %-2d | %-3d | %7.1fMB | %7.4f | %7.4f | %6.1f | %4.1f%% | %5.1f%% | %6.0f | %5.2fx | %6.2fx |\n",
-                            r.fmt.c_str(), L, G, r.S, r.bytes / 1e6, r.best_ms, r.mean_ms, gbs,
-                            100.0 * gbs / ceil_gbs, 100.0 * gbs / 8000.0, 1e3 / r.best_ms,
-                            f16_ms > 0 ? f16_ms / r.best_ms : 0.0, f16p_ms > 0 ? f16p_ms / r.best_ms : 0.0);
-                std::fflush(stdout);
-                rows.push_back(r);
+                block.push_back(r);
             }
         }
+        for (const Row& r : block) {
+            const double gbs = r.bytes / (r.best_ms * 1e6);
+            std::printf("| %-4s | %-6d | %-2d | %-3d | %7.1fMB | %7.4f | %7.4f | %6.1f | %4.1f%% | %5.1f%% | %6.0f | %s | %7s |\n",
+                        r.fmt.c_str(), L, G, r.S, r.bytes / 1e6, r.best_ms, r.mean_ms, gbs,
+                        100.0 * gbs / ceil_gbs, 100.0 * gbs / 8000.0, 1e3 / r.best_ms,
+                        ratio(f16_ms, r.best_ms).c_str(), ratio(f16p_ms, r.best_ms).c_str());
+            rows.push_back(r);
+        }
+        std::fflush(stdout);
     }
     check(va_stream_destroy(stream));
     std::printf("\nbytes = compressed K+V payload + fp16 group scales; q/out/workspace excluded.\n");
