@@ -422,9 +422,12 @@ __device__ void finish_counted(const DecodeArgs& a, const Route& rt, const float
             a.out[(size_t)(rt.oh0 + q) * D + t] = s_bad ? (uint16_t)0x7E00u : f2h_rne(r);
         }
     }
-    if (t == 0) {                                // every partial is in: reset for the slot's next call
-        store_dev(line, 0u);
-        store_dev(line + 2, 0u);
+    if (t == 0) {                                // reset for the slot's next call
+        store_dev(line, 0u);                     // every ticket of this call is taken
+        // The S - 1 counts waited for are taken back rather than the word
+        // zeroed: after a poll that gave up (NaN output), a count still on its
+        // way then brings the word back to 0 instead of into the next call.
+        __hip_atomic_fetch_sub(line + 2, (unsigned)(S - 1), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
 }
 
