@@ -25,15 +25,16 @@ __device__ __forceinline__ uint64_t tagged(float v, uint32_t tag) {
     return ((uint64_t)tag << 32) | __builtin_bit_cast(uint32_t, v);
 }
 
-// 16 bytes (two tagged words) from the device coherence point (sc1, as the
-// relaxed agent-scope loads of va_device.hpp). The compiler tracks these like
-// any buffer load, so a round of them is in flight at once.
+// 16 bytes (two tagged words, or four plain floats) from the device coherence
+// point (sc1, as the relaxed agent-scope loads of va_device.hpp). The compiler
+// tracks these like any buffer load, so a round of them is in flight at once.
 __device__ __forceinline__ u32x4 ld128_dev(__amdgpu_buffer_rsrc_t r, uint32_t voff) {
     return __builtin_amdgcn_raw_buffer_load_b128(r, voff, 0, 16 /* sc1 */);
 }
 
-// The call epoch of merge group mg on this call's ticket slot; read at kernel
-// start (the merge of this call advances it only after every group arrived).
+// The call epoch of merge group mg on this call's ticket slot (the tagged
+// protocol's tags); read at kernel start (the merge of this call advances it
+// only after every group arrived).
 __device__ __forceinline__ unsigned read_epoch(const DecodeArgs& a, int mg) {
     if (a.ticket_slot < 0) return 0u;
     return load_dev(g_tickets + ((size_t)a.ticket_slot * TICKET_MAXH + mg) * TICKET_STRIDE + 1);
