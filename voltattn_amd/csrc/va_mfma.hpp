@@ -450,11 +450,14 @@ __global__ __launch_bounds__(WAVES * 64, 1) void decode_mfma(DecodeArgs a) {
             __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
         };
 
+        // Tiles in pairs; an odd count leaves after its last tile (niter is
+        // uniform over the work-group; the prefetch past the split reads nothing).
         const int npair = (niter + 1) / 2;
         for (int ip = 0; ip < npair; ++ip) {
             const int it = 2 * ip;
             load_tile(it + 1, kb, vb, skb, svb);
             compute_tile(it, ka, va_, ska, sva);
+            if (it + 1 >= niter) break;
             load_tile(it + 2, ka, va_, ska, sva);
             compute_tile(it + 1, kb, vb, skb, svb);
         }

@@ -273,16 +273,17 @@ __global__ __launch_bounds__(WAVES * 64, MINB) void decode_tiled(DecodeArgs a) {
             }
         };
 
-        // Tiles are processed in pairs. Loads past the end of the split return
-        // zeros without memory traffic and their scores are masked, so the
-        // prefetch after the last tile and the empty tile that completes an
-        // odd count add no traffic and leave (m, l, o) unchanged.
+        // Tiles are processed in pairs; an odd count leaves the loop after its
+        // last tile (niter is uniform over the work-group). Loads past the end
+        // of the split return zeros without memory traffic, so the prefetch
+        // after the last tile adds no traffic.
         const int npair = (niter + 1) / 2;
         for (int ip = 0; ip < npair; ++ip) {
             const int it = 2 * ip;
             stage_scales(ska, sva);
             load_tile(it + 1, kb, vb, skb, svb);
             compute_tile(it, ka, va_);
+            if (it + 1 >= niter) break;
             stage_scales(skb, svb);
             load_tile(it + 2, ka, va_, ska, sva);
             compute_tile(it + 1, kb, vb);
