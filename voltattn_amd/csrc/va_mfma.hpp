@@ -122,6 +122,8 @@ __global__ __launch_bounds__(WAVES * 64, 1) void decode_mfma(DecodeArgs a) {
     __shared__ float s_red[QG][WAVES][D];
     __shared__ float s_l[QG][WAVES];
     __shared__ float s_m[QG][WAVES];
+    __shared__ float s_acc[QG][D];
+    __shared__ float s_mf[QG], s_lf[QG];
     __shared__ int   s_page[PAGED ? MAX_SPLIT_PAGES : 1];
 
     // ---- work-group -> (sequence b, KV head hk, query sub-group, split s)
@@ -471,42 +473,61 @@ __global__ __launch_bounds__(WAVES * 64, 1) void decode_mfma(DecodeArgs a) {
         s_l[lane][wave] = lt;
         s_m[lane][wave] = mq;
     }
+    // Row (grp, cq) of this lane's accumulators holds its useful dimensions in
+    // the JB column blocks of scale group grp (grp depends on the quarter g):
+    // the blocks are picked by selects, not branches.
+    constexpr int JB = G / 16;                       // column blocks per scale group
 #pragma unroll
     for (int v = 0; v < 4; ++v) {
         const int r = 4 * g + v;                     // stacked row (r / QP, r % QP)
+        const int grp = r / QP, cq_r = QP == 4 ? v : r % QP;
         const float er = __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute(r << 2, __builtin_bit_cast(int, ex)));
         const float f  = __builtin_bit_cast(float, (uint32_t)(127 - (int)er) << 23);
+        if (cq_r < QG) {
 #pragma unroll
-        for (int nb = 0; nb < NB; ++nb) {
-            // q8: block nb is dimensions 16nb + col; q4: byte column 16(nb/2) + col,
-            // low nibble (even dimension) or high nibble (odd, accumulated as 16v)
-            const int d = !Q4 ? 16 * nb + col : 2 * (16 * (nb >> 1) + col) + (nb & 1);
-            const float fh = (Q4 && (nb & 1)) ? f * 0.0625f : f;
-            if (r / QP == d / G && r % QP < QG) s_red[r % QP][wave][d] = o[nb][v] * fh;
+            for (int j = 0; j < JB; ++j) {
+                float val = o[j][v];
+#pragma unroll
+                for (int gg = 1; gg < NG; ++gg) val = grp == gg ? o[gg * JB + j][v] : val;
+                // q8: block nb is dimensions 16nb + col; q4: byte column 16(nb/2) + col,
+                // low nibble (even dimension) or high nibble (odd, accumulated as 16v)
+                const int nb = grp * JB + j;
+                const int d = !Q4 ? 16 * nb + col : 2 * (16 * (nb >> 1) + col) + (j & 1);
+                s_red[cq_r][wave][d] = val * ((Q4 && (j & 1)) ? f * 0.0625f : f);
+            }
         }
     }
     bool any_bad = false;
     if constexpr (PAGED) any_bad = __syncthreads_or(bad);
     else __syncthreads();
+    // fold the WAVES partials of each (query slot, dimension), one per thread
     const int t = (int)threadIdx.x;
+    static_assert(QG * D <= WAVES * 64, "one thread per (query slot, dimension)");
+    if (t < QG * D) {
+        const int q = t / D, d = t - (t / D) * D;
+        float m = s_m[q][0];
+#pragma unroll
+        for (int w = 1; w < WAVES; ++w) m = fmaxf(m, s_m[q][w]);
+        float sacc = 0.f, sl = 0.f;
+#pragma unroll
+        for (int w = 0; w < WAVES; ++w) {
+            const float f = fast_exp2(s_m[q][w] - m);
+            sacc = __builtin_fmaf(f, s_red[q][w][d], sacc);
+            sl   = __builtin_fmaf(f, s_l[q][w], sl);
+        }
+        s_acc[q][d] = sacc;
+        if (d == 0) {
+            s_mf[q] = m;
+            s_lf[q] = any_bad ? __builtin_nanf("") : sl;
+        }
+    }
+    __syncthreads();
     float M[QG], acc[QG], ls[QG];
 #pragma unroll
     for (int q = 0; q < QG; ++q) {
-        M[q] = 0.f;
-        acc[q] = 0.f;
-        ls[q] = 0.f;
-        if (t < D) {
-            M[q] = s_m[q][0];
-#pragma unroll
-            for (int w = 1; w < WAVES; ++w) M[q] = fmaxf(M[q], s_m[q][w]);
-#pragma unroll
-            for (int w = 0; w < WAVES; ++w) {
-                const float f = fast_exp2(s_m[q][w] - M[q]);
-                acc[q] = __builtin_fmaf(f, s_red[q][w][t], acc[q]);
-                ls[q]  = __builtin_fmaf(f, s_l[q][w], ls[q]);
-            }
-            if (any_bad) ls[q] = __builtin_nanf("");
-        }
+        M[q] = s_mf[q];
+        ls[q] = s_lf[q];
+        acc[q] = t < D ? s_acc[q][t] : 0.f;
     }
     finish_partial<D, WAVES * 64, QG>(a, rt, M, ls, acc, epoch);
 }
