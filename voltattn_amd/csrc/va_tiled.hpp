@@ -322,23 +322,57 @@ __global__ __launch_bounds__(WAVES * 64, MINB) void decode_tiled(DecodeArgs a) {
     else __syncthreads();
     const int t = (int)threadIdx.x;
     float M[QG], acc[QG], ls[QG];
+    if constexpr (QG < 4) {
+        // threads t < D fold every query slot of dimension t (measured faster
+        // than the all-thread fold below up to two slots)
 #pragma unroll
-    for (int q = 0; q < QG; ++q) {
-        M[q] = 0.f;
-        acc[q] = 0.f;
-        ls[q] = 0.f;
-        if (t < D) {
-            M[q] = s_m[q][0];
+        for (int q = 0; q < QG; ++q) {
+            M[q] = 0.f;
+            acc[q] = 0.f;
+            ls[q] = 0.f;
+            if (t < D) {
+                M[q] = s_m[q][0];
 #pragma unroll
-            for (int w = 1; w < WAVES; ++w) M[q] = fmaxf(M[q], s_m[q][w]);
+                for (int w = 1; w < WAVES; ++w) M[q] = fmaxf(M[q], s_m[q][w]);
+                float f[WAVES];
+#pragma unroll
+                for (int w = 0; w < WAVES; ++w) f[w] = fast_exp2(s_m[q][w] - M[q]);
+#pragma unroll
+                for (int r = 0; r < WAVES * 4; ++r) acc[q] = __builtin_fmaf(f[r / 4], s_red[q][r][t], acc[q]);
+#pragma unroll
+                for (int r = 0; r < WAVES * 4; ++r) ls[q] = __builtin_fmaf(f[r / 4], s_l[q][r], ls[q]);
+                if (any_bad) ls[q] = __builtin_nanf("");
+            }
+        }
+    } else {
+        // four query slots: every thread folds (query slot, dimension) pairs
+        __shared__ float s_acc[QG][D];
+        __shared__ float s_mf[QG], s_lf[QG];
+        for (int i = t; i < QG * D; i += WAVES * 64) {
+            const int q = i / D, d = i - (i / D) * D;
+            float m = s_m[q][0];
+#pragma unroll
+            for (int w = 1; w < WAVES; ++w) m = fmaxf(m, s_m[q][w]);
             float f[WAVES];
 #pragma unroll
-            for (int w = 0; w < WAVES; ++w) f[w] = fast_exp2(s_m[q][w] - M[q]);
+            for (int w = 0; w < WAVES; ++w) f[w] = fast_exp2(s_m[q][w] - m);
+            float sacc = 0.f, sl = 0.f;
 #pragma unroll
-            for (int r = 0; r < WAVES * 4; ++r) acc[q] = __builtin_fmaf(f[r / 4], s_red[q][r][t], acc[q]);
+            for (int r = 0; r < WAVES * 4; ++r) sacc = __builtin_fmaf(f[r / 4], s_red[q][r][d], sacc);
+            s_acc[q][d] = sacc;
+            if (d == 0) {
 #pragma unroll
-            for (int r = 0; r < WAVES * 4; ++r) ls[q] = __builtin_fmaf(f[r / 4], s_l[q][r], ls[q]);
-            if (any_bad) ls[q] = __builtin_nanf("");
+                for (int r = 0; r < WAVES * 4; ++r) sl = __builtin_fmaf(f[r / 4], s_l[q][r], sl);
+                s_mf[q] = m;
+                s_lf[q] = any_bad ? __builtin_nanf("") : sl;
+            }
+        }
+        __syncthreads();
+#pragma unroll
+        for (int q = 0; q < QG; ++q) {
+            M[q] = s_mf[q];
+            ls[q] = s_lf[q];
+            acc[q] = t < D ? s_acc[q][t] : 0.f;
         }
     }
     finish_partial<D, WAVES * 64, QG>(a, rt, M, ls, acc, epoch);
