@@ -31,7 +31,7 @@ __global__ __launch_bounds__(256) void decode_w1(DecodeArgs a) {
     const int wg   = blockIdx.x;
     const int h    = wg / a.S;
     const int s    = wg - h * a.S;
-    const unsigned epoch = read_epoch(a, h);
+    const unsigned epoch = read_epoch<1>(a, h);
     const Route rt{h, s, 1, h};
     const int wave = (int)(threadIdx.x >> 6);
     const int lane = (int)(threadIdx.x & 63);

@@ -34,8 +34,12 @@ __device__ __forceinline__ u32x4 ld128_dev(__amdgpu_buffer_rsrc_t r, uint32_t vo
 
 // The call epoch of merge group mg on this call's ticket slot (the tagged
 // protocol's tags); read at kernel start (the merge of this call advances it
-// only after every group arrived).
+// only after every group arrived). Only the tagged protocol (one query slot)
+// uses it: with several slots nothing is read, so no coherent load sits in
+// front of the work-group's first tile.
+template <int QG>
 __device__ __forceinline__ unsigned read_epoch(const DecodeArgs& a, int mg) {
+    if constexpr (QG > 1) return 0u;
     if (a.ticket_slot < 0) return 0u;
     return load_dev(g_tickets + ((size_t)a.ticket_slot * TICKET_MAXH + mg) * TICKET_STRIDE + 1);
 }

@@ -136,7 +136,7 @@ __global__ __launch_bounds__(WAVES * 64, 1) void decode_mfma(DecodeArgs a) {
     rt.nq  = min(QG, a.qgroup - sub * QG);
     rt.oh0 = (b * a.hkv + hk) * a.qgroup + sub * QG;
     const int s = rt.s;
-    const unsigned epoch = read_epoch(a, rt.mg);
+    const unsigned epoch = read_epoch<QG>(a, rt.mg);
     const int wave = uniform((int)(threadIdx.x >> 6));
     const int lane = (int)(threadIdx.x & 63);
     const int g    = lane >> 4;                  // quarter
@@ -232,6 +232,21 @@ __global__ __launch_bounds__(WAVES * 64, 1) void decode_mfma(DecodeArgs a) {
             __builtin_amdgcn_sched_barrier(0);
         };
 
+        // This lane's q words are loaded ahead of tile 0: vector loads complete
+        // in order, so the digit arithmetic below then overlaps the tile's
+        // latency instead of waiting for it. (Words are taken out of each vector
+        // right after its load.)
+        constexpr int EPQ = D / 4;                // dimensions of a lane quarter
+        uint32_t qwd[EPQ / 2];
+        {
+            const _Float16* qrow = reinterpret_cast<const _Float16*>(a.q) + (size_t)(rt.oh0 + (cq < rt.nq ? cq : 0)) * D;
+#pragma unroll
+            for (int i = 0; i < EPQ / 8; ++i) {
+                const u32x4 w = *reinterpret_cast<const u32x4*>(qrow + g * EPQ + 8 * i);
+                qwd[4 * i] = w.x; qwd[4 * i + 1] = w.y; qwd[4 * i + 2] = w.z; qwd[4 * i + 3] = w.w;
+            }
+        }
+        __builtin_amdgcn_sched_barrier(0);
         load_tile(0, ka, va_, ska, sva);
 
         // q^T operand of the q.K products: column (cg, cq); k slots of quarter g
@@ -245,18 +260,16 @@ __global__ __launch_bounds__(WAVES * 64, 1) void decode_mfma(DecodeArgs a) {
         float cf;                                 // qscale * 2^-sh of this column
         int   qoff[3] = {0, 0, 0};                // q4: -8 * (column sum of each digit)
         {
-            constexpr int EPQ = D / 4;            // dimensions of a lane quarter
             const int e0 = g * EPQ;               // they all lie in scale group e0 / G
             const bool use = cq < rt.nq && e0 / G == cg;
-            const _Float16* qrow = reinterpret_cast<const _Float16*>(a.q) + (size_t)(rt.oh0 + (cq < rt.nq ? cq : 0)) * D;
             float qe[EPQ];
             float lmax = 0.f;
 #pragma unroll
             for (int i = 0; i < EPQ / 8; ++i) {
-                const u32x4 w = *reinterpret_cast<const u32x4*>(qrow + e0 + 8 * i);
 #pragma unroll
                 for (int e = 0; e < 8; ++e) {
-                    const uint32_t h = (e & 1) ? (w[e >> 1] >> 16) : (w[e >> 1] & 0xFFFFu);
+                    const uint32_t wd = qwd[4 * i + (e >> 1)];
+                    const uint32_t h = (e & 1) ? (wd >> 16) : (wd & 0xFFFFu);
                     qe[8 * i + e] = use ? h2f(h) : 0.f;
                     lmax = fmaxf(lmax, fabsf(qe[8 * i + e]));
                 }

@@ -89,7 +89,7 @@ __global__ __launch_bounds__(WAVES * 64, MINB) void decode_tiled(DecodeArgs a) {
         rt.oh0 = (b * a.hkv + hk) * a.qgroup + sub * QG;
     }
     const int s = rt.s;
-    const unsigned epoch = read_epoch(a, rt.mg);
+    const unsigned epoch = read_epoch<QG>(a, rt.mg);
     const int wave = uniform((int)(threadIdx.x >> 6));
     const int lane = (int)(threadIdx.x & 63);
     const int sl   = lane % LP;                  // lane within its row
