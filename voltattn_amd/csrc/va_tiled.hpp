@@ -273,20 +273,25 @@ __global__ __launch_bounds__(WAVES * 64, MINB) void decode_tiled(DecodeArgs a) {
             }
         };
 
-        // Tiles are processed in pairs; an odd count leaves the loop after its
-        // last tile (niter is uniform over the work-group). Loads past the end
-        // of the split return zeros without memory traffic, so the prefetch
-        // after the last tile adds no traffic.
-        const int npair = (niter + 1) / 2;
+        // Tiles are processed in pairs, and an odd last tile after the loop (its
+        // loads are the last pair's prefetch; niter is uniform over the
+        // work-group). Loads past the end of the split return zeros without
+        // memory traffic, so the prefetch after the last tile adds no traffic.
+        // (An exit inside the loop instead measured 1.5 us slower for the paged
+        // one-slot form: it changes how the loop body is scheduled.)
+        const int npair = niter / 2;
         for (int ip = 0; ip < npair; ++ip) {
             const int it = 2 * ip;
             stage_scales(ska, sva);
             load_tile(it + 1, kb, vb, skb, svb);
             compute_tile(it, ka, va_);
-            if (it + 1 >= niter) break;
             stage_scales(skb, svb);
             load_tile(it + 2, ka, va_, ska, sva);
             compute_tile(it + 1, kb, vb);
+        }
+        if (niter & 1) {
+            stage_scales(ska, sva);
+            compute_tile(niter - 1, ka, va_);
         }
 #pragma unroll
         for (int q = 0; q < QG; ++q) C::finish(o[q]);
