@@ -245,15 +245,16 @@ __device__ void finish_tagged(const DecodeArgs& a, const Route& rt, const float 
     }
 }
 
-// Counted protocol: thread NT-1 takes the merge group's ticket first (word 0 of the
-// group's ticket line). A work-group that does not complete the ticket stores
-// its partials as plain fp32 (o[0..D), m, l; PSF floats each, partial (q, s) of
-// merge group mg at (mg*QG + q)*S + s) with device-coherent stores, waits
-// until they have completed (every thread, then the barrier) and counts itself
-// in word 2 of the line. The work-group that completes the ticket keeps its own
-// partials in LDS, waits (bounded) until the other S-1 have counted, and
-// merges: it waits only for groups that have already taken their ticket, so
-// every wait ends.
+// Counted protocol: every work-group stores its partials as plain fp32 (o[0..D),
+// m, l; PSF floats each, partial (q, s) of merge group mg at (mg*QG + q)*S + s)
+// with device-coherent stores while thread NT-1 takes the merge group's ticket
+// (word 0 of the group's ticket line), so the stores' round trip overlaps the
+// ticket's. Every thread then waits until its stores (or the atomic) have
+// completed, and after the barrier a work-group that did not complete the
+// ticket counts itself in word 2 of the line. The work-group that completes the
+// ticket merges from its own partials in LDS (its stores go unused), after
+// waiting (bounded) until the other S-1 have counted: it waits only for groups
+// that have already taken their ticket, so every wait ends.
 //
 // The merge spreads the loads over all NT/64 waves and runs the query slots
 // side by side: WQ = NW/QG waves per slot; lane j of each of them reads split
@@ -282,28 +283,27 @@ __device__ void finish_counted(const DecodeArgs& a, const Route& rt, const float
     __shared__ float s_fold[QG][WQ][D];
     __shared__ float s_lsum[QG];
     unsigned* line = g_tickets + ((size_t)a.ticket_slot * TICKET_MAXH + rt.mg) * TICKET_STRIDE;
+    float* base = g_partf + (size_t)a.ticket_slot * PART_CAP * PARTF_STRIDE + (size_t)rt.mg * QG * S * PSF;
+    if (t < D) {
+#pragma unroll
+        for (int q = 0; q < QG; ++q) {
+            if (q >= rt.nq) break;
+            float* mine = base + ((size_t)q * S + s) * PSF;
+            store_dev(mine + t, acc[q]);
+            if (t == 0) {
+                store_dev(mine + D, M[q]);
+                store_dev(mine + D + 1, ls[q]);
+            }
+        }
+    }
     if (t == NT - 1)
         s_last = __hip_atomic_fetch_add(line, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
                  (unsigned)(S - 1);
+    // The stores are written through to the device coherence point (sc1): once
+    // each thread has seen its own complete, the count may go up.
+    wait_all_mem();
     __syncthreads();
-    float* base = g_partf + (size_t)a.ticket_slot * PART_CAP * PARTF_STRIDE + (size_t)rt.mg * QG * S * PSF;
     if (!s_last) {
-        if (t < D) {
-#pragma unroll
-            for (int q = 0; q < QG; ++q) {
-                if (q >= rt.nq) break;
-                float* mine = base + ((size_t)q * S + s) * PSF;
-                store_dev(mine + t, acc[q]);
-                if (t == 0) {
-                    store_dev(mine + D, M[q]);
-                    store_dev(mine + D + 1, ls[q]);
-                }
-            }
-        }
-        // The stores are written through to the device coherence point (sc1):
-        // once each thread has seen its own complete, the count may go up.
-        wait_all_mem();
-        __syncthreads();
         if (t == 0) __hip_atomic_fetch_add(line + 2, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         return;
     }
