@@ -35,7 +35,7 @@
 extern "C" {
 #endif
 
-#define VA_ABI_VERSION 2
+#define VA_ABI_VERSION 3
 
 /* Status codes. */
 enum {
@@ -45,7 +45,8 @@ enum {
     VA_ENULL    = 3,  /* a required pointer is NULL */
     VA_ERANGE   = 4,  /* shape exceeds the 32-bit buffer addressing of a head */
     VA_EHIP     = 5,  /* HIP runtime or launch error */
-    VA_ENODEV   = 6   /* no usable gfx950 device */
+    VA_ENODEV   = 6,  /* no usable gfx950 device */
+    VA_ELOST    = 7   /* a fused merge gave up waiting for a partial (va_merge_faults) */
 };
 
 /* Formats: the reference's enum class Fmt {F16, F16M, Q8, Q8M, Q4, Q4M, Q3M}
@@ -80,8 +81,22 @@ typedef struct {
  * fp16 output. Replaces launch() (src/voltattn.cu:803-835), adding the group
  * size G (the reference fixes GROUP = 64, src/voltattn.cu:60).
  * Valid: D in {64,128}; G in {32,64} with G <= D (ignored for f16 formats);
- * H >= 1; L >= 1; S >= 1. Asynchronous on `stream`. */
+ * H >= 1; L >= 1; S >= 1. Asynchronous on `stream`.
+ * The merge normally runs inside the decode kernel on a ticket slot of
+ * library memory bound to `stream` (one slot per stream, and one per stream
+ * and capture sequence while a graph is captured; 16 per device). Calls on
+ * different streams may run concurrently; replays of one captured graph must
+ * be ordered after each other (as every launch of one executable graph is).
+ * With H > 1024, S > 64, H*S > 2048, or all 16 slots bound to other streams,
+ * the partials go to ws and a separate merge kernel follows. */
 int va_decode(va_fmt fmt, const va_bufs* b, int H, int L, int D, int G, int S, void* stream);
+
+/* Fused merges on the current device that gave up waiting for a partial
+ * (bounded poll exhausted; the affected outputs were set to NaN) since the
+ * previous call. Synchronizes `stream` first. Returns VA_ELOST with *count > 0
+ * if there were any, else VA_OK with *count = 0. No counterpart in the
+ * reference, whose merge is a separate kernel. */
+int va_merge_faults(void* stream, unsigned* count);
 
 /* First pass only: writes the S partials (m, l, o[D]) per head into b->ws
  * (the attention kernels of launch(), src/voltattn.cu:813-833). `out` unused. */
@@ -237,6 +252,8 @@ int va_memcpy_d2d(void* dst, const void* src, size_t bytes, void* stream);
 int va_memset(void* p, int value, size_t bytes);
 int va_sync(void);
 int va_stream_create(void** stream);
+/* Waits for the stream's work, frees the fused-merge ticket slot bound to it
+ * (va_decode), then destroys it. */
 int va_stream_destroy(void* stream);
 int va_stream_sync(void* stream);
 int va_event_create(void** ev);
@@ -248,8 +265,10 @@ int va_event_elapsed_ms(void* start, void* stop, float* ms);
 /* HIP graph capture of a launch sequence on a (non-default) stream: the
  * reference launches every step from the host; a serving loop would replay
  * captured decode steps instead. va_graph_end instantiates the captured work;
- * va_graph_launch replays it on `stream`. No memset nodes are captured by any
- * entry point of this library. */
+ * va_graph_launch replays it on `stream`; replays of one graph must be ordered
+ * after each other. va_graph_destroy waits for the device and frees the
+ * ticket slots the capture bound (va_decode). No memset nodes are captured by
+ * any entry point of this library. */
 int va_graph_begin(void* stream);
 int va_graph_end(void* stream, void** graph_exec);
 int va_graph_launch(void* graph_exec, void* stream);

@@ -87,10 +87,13 @@ def test_paged_many_sequences_two_pass():
         _check(got[b].ravel(), pb.ref[b].ravel(), b)
 
 
-def test_paged_empty_bad_page_and_overlong_sequence():
-    """Length 0 -> zeros; a page id outside the pool or a length above
-    max_seq_len -> NaN for that sequence only; the others stay exact."""
-    lens = [300, 0, 300, 300]
+@pytest.mark.parametrize("S", [0, 80])              # 0: fused merge; 80 > 64: the merge kernel
+def test_paged_empty_bad_page_and_overlong_sequence(S):
+    """Length 0 -> zeros; a page id outside the pool, a length above
+    max_seq_len or a negative length -> NaN for that sequence only; the others
+    stay exact. Both merge paths (in the decode kernel and the separate
+    lse_merge pass) give the same verdicts."""
+    lens = [300, 0, 300, 300, 0]
     pb = batch_util.PagedBatch(va.Fmt.Q8M, lens, 8, 2, 128, 32, 64, seed=5, max_seq_len=320,
                                max_pages=6)
     try:
@@ -98,13 +101,16 @@ def test_paged_empty_bad_page_and_overlong_sequence():
         table[2, 1] = pb.shape.num_pages + 5          # sequence 2: second page id outside the pool
         seq = pb.seq_lens.copy()
         seq[3] = 321                                  # sequence 3: above max_seq_len
-        got = pb.run(table=table, seq_lens=seq)
+        seq[4] = -5                                   # sequence 4: negative length
+        print(f"paged bad inputs S={S}", flush=True)
+        got = pb.run(S=S, table=table, seq_lens=seq)
     finally:
         pb.free()
     _check(got[0].ravel(), pb.ref[0].ravel(), 0)
     assert np.all(got[1] == 0.0)
     assert np.all(np.isnan(got[2]))
     assert np.all(np.isnan(got[3]))
+    assert np.all(np.isnan(got[4]))
 
 
 def test_contiguous_cache_as_one_page_per_sequence():
@@ -141,11 +147,10 @@ def _special_rows(rng, shape):
     return x.astype(np.float16)
 
 
-@pytest.mark.parametrize("fmt", ALL, ids=lambda f: f.label)
-@pytest.mark.parametrize("G", [32, 64])
+# f16 formats have no scales: one G for them
+@pytest.mark.parametrize("fmt,G", [(f, G) for f in ALL for G in (32, 64) if va.fmt_bits(f) != 16 or G == 32],
+                         ids=lambda x: x.label if isinstance(x, va.Fmt) else str(x))
 def test_append_is_bit_exact(fmt, G):
-    if va.fmt_bits(fmt) == 16 and G == 64:
-        pytest.skip("f16 formats have no scales")
     rng = np.random.default_rng(G + int(fmt))
     B, Hkv, D, P, n = 3, 2, 128, 16, 37
     start = np.array([0, 5, 30], np.int32)

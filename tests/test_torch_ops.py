@@ -1,6 +1,7 @@
 """The torch.library binding without a GPU: the ops are registered under
 torch.ops.voltattn, their fake (meta) implementations give the documented
-output shapes, and CPU tensors are refused loudly (no CPU fallback)."""
+output shapes and reject every tensor whose shape or dtype does not match
+(fmt, D, G), and CPU tensors are refused loudly (no CPU fallback)."""
 import pytest
 import torch
 
@@ -18,8 +19,9 @@ def test_fake_shapes_on_meta():
     k = torch.empty(8, 4096, 128, dtype=torch.uint8, **m)
     s = torch.empty(8, 4096, 4, dtype=torch.float16, **m)
     assert torch.ops.voltattn.decode_gqa(q, k, k, s, s, "q8+").shape == (32, 128)
-    assert torch.ops.voltattn.decode(q, torch.empty(32, 4096, 128, dtype=torch.uint8, **m), k, s, s,
-                                     "q8+").shape == (32, 128)
+    k32 = torch.empty(32, 4096, 128, dtype=torch.uint8, **m)
+    s32 = torch.empty(32, 4096, 4, dtype=torch.float16, **m)
+    assert torch.ops.voltattn.decode(q, k32, k32, s32, s32, "q8+").shape == (32, 128)
     qb = torch.empty(4, 32, 128, dtype=torch.float16, **m)
     pages = torch.empty(64, 8, 256, 64, dtype=torch.uint8, **m)
     sp = torch.empty(64, 8, 256, 4, dtype=torch.float16, **m)
@@ -39,3 +41,97 @@ def test_cpu_tensors_refused():
         torch.ops.voltattn.decode(q, k, k, s, s, "q8+")
     with pytest.raises(RuntimeError, match="gfx950"):
         torch.ops.voltattn.quantize(torch.zeros(2, 128), 8, 32)
+
+
+M = dict(device="meta")
+
+
+def _t(*shape, dtype=torch.uint8):
+    return torch.empty(*shape, dtype=dtype, **M)
+
+
+def _decode_args(**over):
+    a = dict(q=_t(8, 128, dtype=torch.float16), k=_t(8, 256, 64), v=_t(8, 256, 64),
+             ks=_t(8, 256, 4, dtype=torch.float16), vs=_t(8, 256, 4, dtype=torch.float16))
+    a.update(over)
+    return a
+
+
+@pytest.mark.parametrize("over,msg", [
+    (dict(q=_t(8, 128, dtype=torch.float32)), "q has dtype"),
+    (dict(q=_t(8, 96, dtype=torch.float16)), "D must be 64 or 128"),
+    (dict(k=_t(8, 256, 128)), "k has shape"),                      # q8 row bytes, not q4
+    (dict(v=_t(8, 255, 64)), "v has shape"),
+    (dict(k=_t(4, 256, 64), v=_t(4, 256, 64)), "k has 4 heads"),
+    (dict(ks=_t(8, 256, 2, dtype=torch.float16)), "k_scale has shape"),
+    (dict(vs=_t(8, 256, 4, dtype=torch.float32)), "v_scale has dtype"),
+    (dict(ks=None), "k_scale is required"),
+])
+def test_decode_rejects_mismatched_tensors(over, msg):
+    a = _decode_args(**over)
+    with pytest.raises(RuntimeError, match=msg):
+        torch.ops.voltattn.decode(a["q"], a["k"], a["v"], a["ks"], a["vs"], "q4+", 32)
+
+
+def test_decode_f16_and_gqa_checks():
+    q = _t(8, 128, dtype=torch.float16)
+    kf = _t(8, 100, 128, dtype=torch.float16)
+    assert torch.ops.voltattn.decode(q, kf, kf, None, None, "f16+").shape == (8, 128)
+    with pytest.raises(RuntimeError, match="k has dtype"):
+        torch.ops.voltattn.decode(q, _t(8, 100, 128), _t(8, 100, 128), None, None, "f16+")
+    k3 = _t(3, 100, 48)
+    s3 = _t(3, 100, 4, dtype=torch.float16)
+    with pytest.raises(RuntimeError, match="multiple of K/V heads"):
+        torch.ops.voltattn.decode_gqa(q, k3, k3, s3, s3, "q3+")
+    with pytest.raises(RuntimeError, match="group must be"):
+        torch.ops.voltattn.decode_gqa(q, _t(2, 100, 48), _t(2, 100, 48), s3[:2], s3[:2], "q3+", 48)
+
+
+def _paged_args(**over):
+    a = dict(q=_t(2, 8, 128, dtype=torch.float16), kp=_t(16, 2, 64, 128), vp=_t(16, 2, 64, 128),
+             ksp=_t(16, 2, 64, 4, dtype=torch.float16), vsp=_t(16, 2, 64, 4, dtype=torch.float16),
+             bt=_t(2, 8, dtype=torch.int32), sl=_t(2, dtype=torch.int32))
+    a.update(over)
+    return a
+
+
+@pytest.mark.parametrize("over,msg", [
+    (dict(kp=_t(16, 3, 64, 128), vp=_t(16, 3, 64, 128)), "multiple of K/V heads"),
+    (dict(vp=_t(16, 2, 64, 64)), "v has shape"),
+    (dict(ksp=_t(16, 2, 32, 4, dtype=torch.float16)), "k_scale has shape"),
+    (dict(bt=_t(3, 8, dtype=torch.int32)), "block_table must be"),
+    (dict(bt=_t(2, 8, dtype=torch.int64)), "block_table has dtype"),
+    (dict(sl=_t(3, dtype=torch.int32)), "seq_lens has shape"),
+    (dict(q=_t(2, 8, 128, dtype=torch.bfloat16)), "q has dtype"),
+])
+def test_decode_paged_rejects_mismatched_tensors(over, msg):
+    a = _paged_args(**over)
+    with pytest.raises(RuntimeError, match=msg):
+        torch.ops.voltattn.decode_paged(a["q"], a["kp"], a["vp"], a["ksp"], a["vsp"], a["bt"], a["sl"],
+                                        "q8+", 512)
+
+
+@pytest.mark.parametrize("over,msg", [
+    (dict(pages=_t(16, 4, 64, 64)), "pages hold 4 K/V heads"),      # pool Hkv != x's Hkv
+    (dict(pages=_t(16, 2, 64, 128)), "pages has shape"),            # q8 rows into a q4 pool
+    (dict(scales=_t(16, 2, 64, 2, dtype=torch.float16)), "scale_pages has shape"),
+    (dict(x=_t(2, 2, 5, 128, dtype=torch.float32)), "x has dtype"),
+    (dict(start=_t(3, dtype=torch.int32)), "start has shape"),
+    (dict(bt=_t(2, 8, dtype=torch.int16)), "block_table has dtype"),
+])
+def test_append_rejects_mismatched_tensors(over, msg):
+    a = dict(x=_t(2, 2, 5, 128, dtype=torch.float16), start=_t(2, dtype=torch.int32),
+             bt=_t(2, 8, dtype=torch.int32), pages=_t(16, 2, 64, 64),
+             scales=_t(16, 2, 64, 4, dtype=torch.float16))
+    a.update(over)
+    with pytest.raises(RuntimeError, match=msg):
+        torch.ops.voltattn.append_kv(a["x"], a["start"], a["bt"], a["pages"], a["scales"], "q4+")
+
+
+def test_quantize_rejects_bad_arguments():
+    with pytest.raises(RuntimeError, match="bits must be"):
+        torch.ops.voltattn.quantize(_t(4, 128, dtype=torch.float32), 5, 32)
+    with pytest.raises(RuntimeError, match="x must be fp32"):
+        torch.ops.voltattn.quantize(_t(4, 128, dtype=torch.float16), 8, 32)
+    with pytest.raises(RuntimeError, match="group must be"):
+        torch.ops.voltattn.quantize(_t(4, 96, dtype=torch.float32), 8, 64)

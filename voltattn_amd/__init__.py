@@ -26,14 +26,13 @@ import numpy as np
 __all__ = [
     "Fmt", "DeviceBufs", "VAError", "launch", "decode_splits", "merge", "ws_bytes",
     "payload_bytes", "scale_bytes", "split_chunk", "pick_splits", "quantize", "f32_to_f16",
-    "fill_normal", "probe_read", "device_info", "device_count", "DeviceBuffer", "Event",
+    "fill_normal", "probe_read", "merge_faults", "device_info", "device_count", "DeviceBuffer", "Event",
     "Stream", "Graph", "sync", "lib", "LIB_PATH", "fmt_bits", "is_f16", "check",
     "PagedShape", "PagedBufs", "decode_gqa", "pick_splits_gqa", "decode_paged",
     "pick_splits_paged", "page_bytes", "page_scale_bytes", "append_kv", "row_bytes",
 ]
 
-# VOLTATTN_LIB may name another build of the same library (tuning variants).
-LIB_PATH = Path(os.environ.get("VOLTATTN_LIB") or Path(__file__).resolve().parent / "libvoltattn_hip.so")
+LIB_PATH = Path(__file__).resolve().parent / "libvoltattn_hip.so"
 if not LIB_PATH.exists():
     raise ImportError(
         f"{LIB_PATH} is not built; run `python voltattn_amd/build.py` (needs hipcc for gfx950)")
@@ -95,6 +94,7 @@ def _sig(name, res, *args):
 _sig("va_decode", _I, _I, C.POINTER(_Bufs), _I, _I, _I, _I, _I, _P)
 _sig("va_decode_splits", _I, _I, C.POINTER(_Bufs), _I, _I, _I, _I, _I, _P)
 _sig("va_merge", _I, _P, _P, _I, _I, _I, _P)
+_sig("va_merge_faults", _I, _P, C.POINTER(C.c_uint))
 _sig("va_ws_bytes", _SZ, _I, _I, _I)
 _sig("va_payload_bytes", _SZ, _I, _I, _I, _I)
 _sig("va_scale_bytes", _SZ, _I, _I, _I, _I, _I)
@@ -216,6 +216,15 @@ def decode_splits(f: Fmt, b: DeviceBufs, H: int, L: int, D: int, S: int, G: int 
 
 def merge(ws: int, out: int, H: int, D: int, S: int, stream=None) -> None:
     check(lib.va_merge(ws, out, H, D, S, _stream(stream)))
+
+
+def merge_faults(stream=None) -> int:
+    """Fused merges on the current device that gave up waiting for a partial since
+    the previous query (their outputs are NaN); raises VAError (VA_ELOST = 7) if any.
+    Synchronizes `stream` first."""
+    n = C.c_uint(0)
+    check(lib.va_merge_faults(_stream(stream), C.byref(n)))
+    return n.value
 
 
 def decode_gqa(f: Fmt, b: DeviceBufs, Hq: int, Hkv: int, L: int, D: int, S: int = 0, G: int = 64,

@@ -6,6 +6,10 @@
 
 * ``voltattn_amd/libvoltattn_hip.so`` — the product: gfx950 HIP kernels and the
   C ABI of ``include/voltattn.h`` (hipcc, one object per ``csrc/*.hip``).
+* ``build/variants/libvoltattn_hip_valu.so`` — the same library with the
+  grouped-query q8/q4 kernels in their vector-ALU form (``VA_GQA_MFMA=0``):
+  the comparison build ``tests/test_gpu_valu_form.py`` runs. Only
+  ``va_decode_ex.hip`` differs; the other objects are the product's.
 * ``oracle/liboracle.so`` — the CPU checker (test infrastructure, g++).
 * ``build/voltattn`` — the C++ selftest/bench/probe harness (tests/cli), linked
   against both.
@@ -59,27 +63,57 @@ def _run(cmd: list[str], cwd: Path | None = None) -> None:
         raise RuntimeError(f"command failed ({res.returncode}): {' '.join(cmd)}\n{res.stdout}\n{res.stderr}")
 
 
-def build_library(jobs: int = 8, out: Path = LIB, defines: tuple[str, ...] = ()) -> Path:
-    """Compile csrc/*.hip and link `out`; `defines` (e.g. "VA_LOAD_AUX=2") build a variant."""
-    obj_dir = OBJ if not defines else OBJ / ("v_" + "_".join(d.replace("=", "") for d in defines))
-    obj_dir.mkdir(parents=True, exist_ok=True)
-    srcs = sorted(CSRC.glob("*.hip"))
-    cc = hipcc()
-    dflags = [f"-D{d}" for d in defines]
+VARIANTS = {
+    # name: (translation unit rebuilt with the defines, defines)
+    "valu": ("va_decode_ex.hip", ("VA_GQA_MFMA=0",)),
+}
+VARIANT_DIR = ROOT / "build" / "variants"
 
-    def compile_one(src: Path) -> Path:
-        obj = obj_dir / (src.stem + ".o")
-        _run([cc, *HIPCC_FLAGS, *dflags, "-I", str(ROOT / "include"), "-c", str(src), "-o", str(obj)])
-        return obj
 
-    with cf.ThreadPoolExecutor(max_workers=max(1, jobs)) as ex:
-        objs = list(ex.map(compile_one, srcs))
+def variant_path(name: str) -> Path:
+    return VARIANT_DIR / f"libvoltattn_hip_{name}.so"
+
+
+def _link(cc: str, objs, out: Path) -> Path:
     out = Path(out)
     out.parent.mkdir(parents=True, exist_ok=True)
     tmp = out.with_suffix(".so.tmp")
     _run([cc, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *map(str, objs)])
     os.replace(tmp, out)
     return out
+
+
+def build_library(jobs: int = 8, out: Path = LIB, defines: tuple[str, ...] = (),
+                  variants: tuple[str, ...] = ()) -> Path:
+    """Compile csrc/*.hip and link `out`; `defines` (e.g. "VA_LOAD_AUX=2") build a
+    variant of the whole library; `variants` (names in VARIANTS) also link those
+    comparison libraries from the same objects plus their rebuilt unit."""
+    obj_dir = OBJ if not defines else OBJ / ("v_" + "_".join(d.replace("=", "") for d in defines))
+    obj_dir.mkdir(parents=True, exist_ok=True)
+    srcs = sorted(CSRC.glob("*.hip"))
+    cc = hipcc()
+    dflags = [f"-D{d}" for d in defines]
+    jobs_list = [(src, obj_dir / (src.stem + ".o"), dflags) for src in srcs]
+    for name in variants:
+        unit, vdefs = VARIANTS[name]
+        vdir = obj_dir / f"variant_{name}"
+        vdir.mkdir(parents=True, exist_ok=True)
+        jobs_list.append((CSRC / unit, vdir / (Path(unit).stem + ".o"), dflags + [f"-D{d}" for d in vdefs]))
+
+    def compile_one(job) -> Path:
+        src, obj, fl = job
+        _run([cc, *HIPCC_FLAGS, *fl, "-I", str(ROOT / "include"), "-c", str(src), "-o", str(obj)])
+        return obj
+
+    with cf.ThreadPoolExecutor(max_workers=max(1, jobs)) as ex:
+        objs = list(ex.map(compile_one, jobs_list))
+    main_objs = objs[:len(srcs)]
+    _link(cc, main_objs, out)
+    for i, name in enumerate(variants):
+        unit = VARIANTS[name][0]
+        vobjs = [o for o in main_objs if o.stem != Path(unit).stem] + [objs[len(srcs) + i]]
+        _link(cc, vobjs, variant_path(name))
+    return Path(out)
 
 
 def build_oracle() -> Path:
@@ -105,7 +139,7 @@ def build_cli() -> Path:
 
 
 def build_all(jobs: int = 8) -> None:
-    build_library(jobs)
+    build_library(jobs, variants=tuple(VARIANTS))
     build_oracle()
     if (ROOT / "tests" / "cli" / "voltattn_cli.cpp").exists():
         build_cli()

@@ -9,7 +9,6 @@
 #include "va_tiled.hpp"
 
 #include <algorithm>
-#include <cstdlib>
 
 namespace va {
 
@@ -115,79 +114,84 @@ __global__ __launch_bounds__(256) void decode_w1(DecodeArgs a) {
 // Tiled configuration per kind: waves per group and tile depth (UnrollSet a or
 // b), measured at H=32 D=128 over L = 4K..64K on MI355X. Every default keeps
 // the same bytes in flight per CU (8 waves x depth a); fewer, deeper groups
-// mean fewer partials to merge and a shorter dispatch. VA_WAVES=4|8 and
-// VA_UNROLL=a|b in the environment override the defaults (tuning switches,
-// read once).
-struct TiledCfg { int waves; bool deep; };
+// mean fewer partials to merge and a shorter dispatch. The configuration is
+// fixed at compile time (VA_<KIND>_WAVES = 4|8, VA_<KIND>_DEEP = 0|1 build
+// variants); only the configured kernel of each kind is built.
+#ifndef VA_F16_WAVES
+#define VA_F16_WAVES 8               // 8 waves x 4 rows
+#endif
+#ifndef VA_F16_DEEP
+#define VA_F16_DEEP 0
+#endif
+#ifndef VA_Q8_WAVES
+#define VA_Q8_WAVES 4                // 4 waves x 4 rows
+#endif
+#ifndef VA_Q8_DEEP
+#define VA_Q8_DEEP 1
+#endif
+#ifndef VA_Q4_WAVES
+#define VA_Q4_WAVES 4                // 4 waves x 4 rows
+#endif
+#ifndef VA_Q4_DEEP
+#define VA_Q4_DEEP 1
+#endif
+#ifndef VA_Q3_WAVES
+#define VA_Q3_WAVES 8                // 8 waves x 2 rows (128 VGPRs: two waves per SIMD)
+#endif
+#ifndef VA_Q3_DEEP
+#define VA_Q3_DEEP 0
+#endif
 
-static TiledCfg default_cfg(int kind) {
-    switch (kind) {
-        case KF16: return {8, false};    // 8 waves x 4 rows
-        case KQ8:  return {4, true};     // 4 waves x 4 rows
-        case KQ4:  return {4, true};     // 4 waves x 4 rows
-        default:   return {8, false};    // q3: 8 waves x 2 rows (128 VGPRs: two waves per SIMD)
-    }
-}
-
-static TiledCfg tiled_cfg(int kind) {
-    static const int w = [] { const char* e = std::getenv("VA_WAVES");  return e ? e[0] : 0; }();
-    static const int u = [] { const char* e = std::getenv("VA_UNROLL"); return e ? e[0] : 0; }();
-    TiledCfg c = default_cfg(kind);
-    if (w == '4' || w == '8') c.waves = w - '0';
-    if (u == 'a' || u == 'b') c.deep = u == 'b';
-    return c;
-}
-
-template <int KIND> static int unroll_of(bool deep) { return deep ? UnrollSet<KIND>::b : UnrollSet<KIND>::a; }
+template <int KIND> struct TiledCfg;
+template <> struct TiledCfg<KF16> { static constexpr int waves = VA_F16_WAVES; static constexpr bool deep = VA_F16_DEEP; };
+template <> struct TiledCfg<KQ8>  { static constexpr int waves = VA_Q8_WAVES;  static constexpr bool deep = VA_Q8_DEEP; };
+template <> struct TiledCfg<KQ4>  { static constexpr int waves = VA_Q4_WAVES;  static constexpr bool deep = VA_Q4_DEEP; };
+template <> struct TiledCfg<KQ3>  { static constexpr int waves = VA_Q3_WAVES;  static constexpr bool deep = VA_Q3_DEEP; };
+template <int KIND> struct TiledShape {
+    static_assert(TiledCfg<KIND>::waves == 4 || TiledCfg<KIND>::waves == 8, "4 or 8 waves per group");
+    static constexpr int waves = TiledCfg<KIND>::waves;
+    static constexpr int U = TiledCfg<KIND>::deep ? UnrollSet<KIND>::b : UnrollSet<KIND>::a;
+};
 
 template <int KIND, int D>
-static int tiled_positions(const TiledCfg& c) {
-    return Tile<KIND, D>::PPW * unroll_of<KIND>(c.deep) * c.waves;
+static int tiled_positions() {
+    return Tile<KIND, D>::PPW * TiledShape<KIND>::U * TiledShape<KIND>::waves;
 }
 
 template <int KIND>
-static int tiled_groups(const TiledCfg& c) {
-    return std::max(1, 8 * UnrollSet<KIND>::a / (c.waves * unroll_of<KIND>(c.deep)));
+static int tiled_groups() {
+    return std::max(1, 8 * UnrollSet<KIND>::a / (TiledShape<KIND>::waves * TiledShape<KIND>::U));
 }
 
 int tile_positions(int kind, bool tiled, int D) {
     if (!tiled) return WAVES;
-    const TiledCfg c = tiled_cfg(kind);
     switch (kind) {
-        case KF16: return D == 128 ? tiled_positions<KF16, 128>(c) : tiled_positions<KF16, 64>(c);
-        case KQ8:  return D == 128 ? tiled_positions<KQ8, 128>(c)  : tiled_positions<KQ8, 64>(c);
-        case KQ4:  return D == 128 ? tiled_positions<KQ4, 128>(c)  : tiled_positions<KQ4, 64>(c);
-        default:   return D == 128 ? tiled_positions<KQ3, 128>(c)  : tiled_positions<KQ3, 64>(c);
+        case KF16: return D == 128 ? tiled_positions<KF16, 128>() : tiled_positions<KF16, 64>();
+        case KQ8:  return D == 128 ? tiled_positions<KQ8, 128>()  : tiled_positions<KQ8, 64>();
+        case KQ4:  return D == 128 ? tiled_positions<KQ4, 128>()  : tiled_positions<KQ4, 64>();
+        default:   return D == 128 ? tiled_positions<KQ3, 128>()  : tiled_positions<KQ3, 64>();
     }
 }
 
 int groups_per_cu(int kind, bool tiled) {
     if (!tiled) return 8;                 // naive: one position per wave, 32 waves per CU
-    const TiledCfg c = tiled_cfg(kind);
     switch (kind) {
-        case KF16: return tiled_groups<KF16>(c);
-        case KQ8:  return tiled_groups<KQ8>(c);
-        case KQ4:  return tiled_groups<KQ4>(c);
-        default:   return tiled_groups<KQ3>(c);
+        case KF16: return tiled_groups<KF16>();
+        case KQ8:  return tiled_groups<KQ8>();
+        case KQ4:  return tiled_groups<KQ4>();
+        default:   return tiled_groups<KQ3>();
     }
 }
 
 template <int KIND, int D, int G>
 static hipError_t launch_one(bool tiled, int H, const DecodeArgs& a, hipStream_t st) {
-    const dim3 grid((unsigned)(H * a.S)), block(256), block8(512);
+    const dim3 grid((unsigned)(H * a.S));
     if (tiled) {
-        constexpr int UA = UnrollSet<KIND>::a, UB = UnrollSet<KIND>::b;
-        const TiledCfg c = tiled_cfg(KIND);
-        if (c.waves == 8) {
-            if (c.deep) hipLaunchKernelGGL((decode_tiled<KIND, D, G, UB, 8, 1, false>), grid, block8, 0, st, a);
-            else        hipLaunchKernelGGL((decode_tiled<KIND, D, G, UA, 8, 1, false>), grid, block8, 0, st, a);
-        } else {
-            if (c.deep) hipLaunchKernelGGL((decode_tiled<KIND, D, G, UB, 4, 1, false>), grid, block, 0, st, a);
-            else        hipLaunchKernelGGL((decode_tiled<KIND, D, G, UA, 4, 1, false>), grid, block, 0, st, a);
-        }
+        using T = TiledShape<KIND>;
+        hipLaunchKernelGGL((decode_tiled<KIND, D, G, T::U, T::waves, 1, false>), grid, dim3(T::waves * 64), 0, st, a);
     } else {
         if constexpr (KIND == KQ3) return hipErrorInvalidValue;
-        else hipLaunchKernelGGL((decode_w1<KIND, D, G>), grid, block, 0, st, a);
+        else hipLaunchKernelGGL((decode_w1<KIND, D, G>), grid, dim3(256), 0, st, a);
     }
     return hipGetLastError();
 }
@@ -216,5 +220,7 @@ hipError_t launch_decode(int kind, bool tiled, int H, int D, int G, const Decode
         default:   return hipErrorInvalidValue;
     }
 }
+
+hipError_t lost_merges_decode(unsigned* n) { return read_lost_merges(n); }
 
 } // namespace va

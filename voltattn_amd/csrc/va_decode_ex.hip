@@ -13,7 +13,6 @@
 #include "va_mfma.hpp"
 
 #include <algorithm>
-#include <cstdlib>
 
 namespace va {
 
@@ -29,20 +28,20 @@ namespace va {
 #endif
 
 // Matrix-core form (va_mfma.hpp) for q8 and q4 rows with two or more query slots:
-// MFMA_WAVES waves per work-group, 32-row wave tiles. VA_MFMA=0 in the
-// environment selects the VALU form instead (a tuning switch, read once).
+// MFMA_WAVES waves per work-group, 32-row wave tiles. A build with
+// VA_GQA_MFMA=0 runs the vector-ALU form of va_tiled.hpp for them instead (the
+// comparison variant the tests build; the product is built with the default).
 #ifndef VA_MFMA_WAVES
 #define VA_MFMA_WAVES 8
 #endif
+#ifndef VA_GQA_MFMA
+#define VA_GQA_MFMA 1
+#endif
 constexpr int MFMA_WAVES = VA_MFMA_WAVES;
 constexpr int MFMA_TILE  = 32 * MFMA_WAVES;
+constexpr bool MFMA_ON   = VA_GQA_MFMA != 0;
 
-static bool mfma_on() {
-    static const bool on = [] { const char* e = std::getenv("VA_MFMA"); return !(e && e[0] == '0'); }();
-    return on;
-}
-
-static bool mfma_kind(int kind) { return (kind == KQ8 || kind == KQ4) && mfma_on(); }
+static bool mfma_kind(int kind) { return (kind == KQ8 || kind == KQ4) && MFMA_ON; }
 static bool mfma_form(int kind, int qg) { return mfma_kind(kind) && qg >= 2; }
 
 // Query slots per work-group, per kind: the largest QG whose 8-wave form (two
@@ -50,10 +49,13 @@ static bool mfma_form(int kind, int qg) { return mfma_kind(kind) && qg >= 2; }
 // 28/4 at L = 16K-64K): QG = 4 at two waves per SIMD beats QG = 8 at one for
 // f16 and q8 (groups of 8 run as two sub-groups, 12-38% faster), and q4 is
 // fastest at QG = 2 (QG = 4 spills at two waves per SIMD). The matrix-core
-// form carries 4 slots for q4 too. VA_EX_QMAX=1|2|4 lowers the cap (a tuning
-// switch, read once).
+// form carries 4 slots for q4 too. A build with VA_EX_QMAX = 1|2|4 lowers the
+// cap (a tuning variant).
+#ifndef VA_EX_QMAX
+#define VA_EX_QMAX 0
+#endif
 int max_query_slots(int kind) {
-    static const int cap = [] { const char* e = std::getenv("VA_EX_QMAX"); return e ? std::atoi(e) : 0; }();
+    constexpr int cap = VA_EX_QMAX;
     const int q = (kind == KF16 || kind == KQ8 || mfma_kind(kind)) ? 4 : 2;
     return (cap == 1 || cap == 2 || cap == 4) ? std::min(q, cap) : q;
 }
@@ -126,20 +128,20 @@ int tile_positions_ex(int kind, int D) {
 
 template <int KIND, int D, int G, int QG, bool PAGED>
 static hipError_t launch_ex(int groups, const DecodeArgs& a, hipStream_t st) {
-    if constexpr ((KIND == KQ8 || KIND == KQ4) && QG >= 2) {
-        if (mfma_on()) {
-            hipLaunchKernelGGL((decode_mfma<KIND, D, G, MFMA_WAVES, QG, PAGED>),
-                               dim3((unsigned)(groups * a.S)), dim3(MFMA_WAVES * 64), 0, st, a);
-            return hipGetLastError();
-        }
+    if constexpr ((KIND == KQ8 || KIND == KQ4) && QG >= 2 && MFMA_ON) {
+        hipLaunchKernelGGL((decode_mfma<KIND, D, G, MFMA_WAVES, QG, PAGED>),
+                           dim3((unsigned)(groups * a.S)), dim3(MFMA_WAVES * 64), 0, st, a);
+        return hipGetLastError();
+    } else if constexpr (KIND == KQ4 && QG > 2) {
+        return hipErrorInvalidValue;                 // matrix-core form only
+    } else {
+        using Cfg = ExCfg<KIND, QG>;
+        constexpr int U = ex_unroll<KIND, D, QG>();
+        static_assert(Tile<KIND, D>::PPW * U <= 64, "a wave tile must fit the smallest page");
+        hipLaunchKernelGGL((decode_tiled<KIND, D, G, U, Cfg::WAVES, QG, PAGED, Cfg::MINB>),
+                           dim3((unsigned)(groups * a.S)), dim3(Cfg::WAVES * 64), 0, st, a);
+        return hipGetLastError();
     }
-    if constexpr (KIND == KQ4 && QG > 2) return hipErrorInvalidValue;   // matrix-core form only
-    using Cfg = ExCfg<KIND, QG>;
-    constexpr int U = ex_unroll<KIND, D, QG>();
-    static_assert(Tile<KIND, D>::PPW * U <= 64, "a wave tile must fit the smallest page");
-    hipLaunchKernelGGL((decode_tiled<KIND, D, G, U, Cfg::WAVES, QG, PAGED, Cfg::MINB>),
-                       dim3((unsigned)(groups * a.S)), dim3(Cfg::WAVES * 64), 0, st, a);
-    return hipGetLastError();
 }
 
 template <int KIND, int D, int G, bool PAGED>
@@ -193,5 +195,7 @@ hipError_t launch_decode_ex(int kind, int D, int G, int qg, bool paged, int grou
         default:   return hipErrorInvalidValue;
     }
 }
+
+hipError_t lost_merges_ex(unsigned* n) { return read_lost_merges(n); }
 
 } // namespace va

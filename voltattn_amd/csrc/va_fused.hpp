@@ -4,7 +4,8 @@
 //
 // The ticket lines and the partial store are file-static device arrays, so
 // every translation unit that includes this header (one code object each)
-// owns its own set; calls rotate over TICKET_SLOTS slots of them.
+// owns its own set of TICKET_SLOTS slots; the host binds a slot to each stream
+// that calls (va_slots.hpp).
 #pragma once
 #include "va_device.hpp"
 #include "va_kernels.hpp"
@@ -20,6 +21,21 @@ static __device__ __align__(256) uint64_t g_parts[(size_t)TICKET_SLOTS * PART_CA
 static __device__ __align__(256) float g_partf[(size_t)TICKET_SLOTS * PART_CAP * PARTF_STRIDE];
 
 constexpr int POLL_MAX = 1 << 12;   // bound on re-reads of one in-flight word
+
+// Merges of this code object that gave up waiting for a partial (NaN output);
+// read by the host through read_lost_merges().
+static __device__ unsigned g_lost_merges;
+
+static inline hipError_t read_lost_merges(unsigned* n) {
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(g_lost_merges));
+    if (e != hipSuccess) return e;
+    return hipMemcpy(n, p, sizeof(unsigned), hipMemcpyDeviceToHost);
+}
+
+__device__ __forceinline__ void count_lost_merge() {
+    __hip_atomic_fetch_add(&g_lost_merges, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
 
 __device__ __forceinline__ uint64_t tagged(float v, uint32_t tag) {
     return ((uint64_t)tag << 32) | __builtin_bit_cast(uint32_t, v);
@@ -225,9 +241,11 @@ __device__ void finish_tagged(const DecodeArgs& a, const Route& rt, const float 
         }
         if (sw == 0 && lane == 0) s_lsum[qw] = lsum;
     }
-    // A lost partial (never observed within the poll bound) shows as NaN.
+    // A lost partial (never observed within the poll bound) shows as NaN, and
+    // is counted for the host (va_merge_faults).
     if (__builtin_amdgcn_ballot_w64(!good) != 0 && lane == 0) s_bad = 1;
     __syncthreads();
+    if (t == 0 && s_bad) count_lost_merge();
     if (t < D) {
 #pragma unroll
         for (int q = 0; q < QG; ++q) {
@@ -325,6 +343,7 @@ __device__ void finish_counted(const DecodeArgs& a, const Route& rt, const float
             n = load_dev(line + 2);
         }
         s_bad = n < (unsigned)(S - 1);
+        if (s_bad) count_lost_merge();
     }
     __syncthreads();                             // the partial loads below are served from the coherence point (sc1)
 

@@ -38,8 +38,10 @@ struct DecodeArgs {
 // memory (zero at load): word 0 counts the arrivals of the group's
 // work-groups, word 1 is the group's call epoch (tagged protocol), advanced by
 // the merging work-group, word 2 counts the groups whose partials are stored
-// (counted protocol). Calls rotate over TICKET_SLOTS slots, so up to that many
-// decode calls may be in flight on one device at once. Each line is 256 bytes:
+// (counted protocol). A slot belongs to one stream (or one captured stream of
+// a graph) at a time (va_slots.hpp), so calls that may overlap never share
+// one; when a device's TICKET_SLOTS are all bound, further streams use the
+// two-pass form. Each line is 256 bytes:
 // atomics to one line serialize at the memory side, and the S arrivals of every
 // group land together. The partials of a fused call live in library memory
 // (PART_CAP partials per slot: PART_STRIDE 64-bit words tagged, PARTF_STRIDE
@@ -82,6 +84,13 @@ int groups_per_cu(int kind, bool tiled);
 // Positions one work-group of the tiled kernel covers per loop iteration;
 // split lengths that are multiples of it leave no partial tile.
 int tile_positions(int kind, bool tiled, int D);
+
+// Host side: the count of fused merges that gave up waiting for a partial
+// (poll bound exhausted; the output was set to NaN) in the code object of the
+// reference-shape kernels (va_decode.hip) and of the grouped/paged kernels
+// (va_decode_ex.hip). The counters only grow.
+hipError_t lost_merges_decode(unsigned* n);
+hipError_t lost_merges_ex(unsigned* n);
 
 // Second pass: log-sum-exp merge of the S partials of every head, fp16 out.
 hipError_t launch_merge(const float* ws, uint16_t* out, int H, int D, int S,

@@ -2,7 +2,10 @@
 // (m, l, o[D]) written by the decode kernels are merged by log-sum-exp and the
 // normalised output is rounded to fp16 (reference combine, src/voltattn.cu:651-672).
 // m is in log2 units (the decode kernels work with exp2), so the weights are
-// exp2(m_s - max_s m_s). Empty splits carry l = 0 and o = 0 and drop out.
+// exp2(m_s - max_s m_s). Empty splits carry l = 0 and o = 0 and drop out; a
+// head whose merged l is 0 (no positions: a paged sequence of length 0) gets a
+// zero output, as in the fused merge, and a non-finite l (an input the decode
+// kernel flagged with l = NaN) gives NaN.
 //
 // The pass is latency-bound (a few hundred KB in total), so it is laid out for
 // one round of independent loads: a work-group owns 32 output columns of one
@@ -74,7 +77,7 @@ __global__ __launch_bounds__(256) void lse_merge(const float* __restrict__ ws,
             o += s_acc[g][threadIdx.x];
             l += s_l[g];
         }
-        out[(size_t)h * D + d] = f2h_rne(o / l);
+        out[(size_t)h * D + d] = f2h_rne(l == 0.f ? 0.f : o / l);
     }
 }
 

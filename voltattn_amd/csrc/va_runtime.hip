@@ -1,17 +1,21 @@
 // va_runtime.hip — the C ABI (include/voltattn.h): argument validation,
-// format -> kernel dispatch, and the thin HIP runtime shims the host harness
-// uses. This is the only translation unit that calls the HIP runtime API.
+// format -> kernel dispatch, ticket-slot binding, and the thin HIP runtime
+// shims the host harness uses. Apart from the kernel launches and the two
+// lost-merge counter reads (va_fused.hpp), this is the only translation unit
+// that calls the HIP runtime API.
 #include "voltattn.h"
 #include "va_kernels.hpp"
+#include "va_slots.hpp"
 
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
-#include <atomic>
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
+#include <mutex>
+#include <unordered_map>
 
 namespace {
 
@@ -83,12 +87,30 @@ int validate(va_fmt fmt, const va_bufs* b, int H, int L, int D, int G, int S, bo
     return VA_OK;
 }
 
-std::atomic<unsigned> g_ticket_seq{0};
+va::SlotTable<va::TICKET_SLOTS> g_slots;
+// Capture sequence of each graph made by va_graph_end (its slots are released
+// by va_graph_destroy).
+std::mutex g_graph_mu;
+std::unordered_map<void*, unsigned long long> g_graph_capture;
 
-// fused: merge inside the decode kernel (needs H <= TICKET_MAXH, S <= 64 and
-// H*S <= PART_CAP), else the partials are left in ws for a separate merge pass.
+// Ticket slot of a fused call on `stream` (va_slots.hpp: one per eager stream,
+// one per stream and capture sequence while capturing), or -1: no slot free,
+// the call runs the two-pass form.
+int ticket_slot_for(void* stream) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return -1;
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    unsigned long long id = 0;
+    if (hipStreamGetCaptureInfo(as_stream(stream), &cs, &id) != hipSuccess) return -1;
+    const unsigned long long capture = cs == hipStreamCaptureStatusActive ? (id | (1ull << 63)) : 0ull;
+    return g_slots.acquire(dev, reinterpret_cast<uintptr_t>(stream), capture);
+}
+
+// slot >= 0: merge inside the decode kernel on that ticket slot (the caller
+// checked H <= TICKET_MAXH, S <= 64 and H*S <= PART_CAP); -1: the partials
+// are left in ws for a separate merge pass.
 int run_splits(va_fmt fmt, const va_bufs* b, int H, int L, int D, int G, int S, void* stream,
-               bool fused) {
+               int slot) {
     va::DecodeArgs a{};
     a.hkv = H;                    // the reference's shape: one query head per K/V head
     a.qgroup = 1;
@@ -100,7 +122,7 @@ int run_splits(va_fmt fmt, const va_bufs* b, int H, int L, int D, int G, int S, 
     a.q  = b->q;
     a.ws = b->ws;
     a.out = b->out;
-    a.ticket_slot = fused ? (int)(g_ticket_seq.fetch_add(1u) % va::TICKET_SLOTS) : -1;
+    a.ticket_slot = slot;
     a.L = L;
     a.S = S;
     a.chunk  = (L + S - 1) / S;
@@ -175,9 +197,10 @@ int va_pick_splits(va_fmt fmt, int H, int L, int D, int* S) {
 int va_decode(va_fmt fmt, const va_bufs* b, int H, int L, int D, int G, int S, void* stream) {
     int rc = validate(fmt, b, H, L, D, G, S, true);
     if (rc) return rc;
-    const bool fused = H <= va::TICKET_MAXH && S <= 64 && (long long)H * S <= va::PART_CAP;
-    rc = run_splits(fmt, b, H, L, D, G, S, stream, fused);
-    if (rc || fused) return rc;
+    const bool fits = H <= va::TICKET_MAXH && S <= 64 && (long long)H * S <= va::PART_CAP;
+    const int slot = fits ? ticket_slot_for(stream) : -1;
+    rc = run_splits(fmt, b, H, L, D, G, S, stream, slot);
+    if (rc || slot >= 0) return rc;
     const hipError_t e = va::launch_merge(b->ws, b->out, H, D, S, as_stream(stream));
     if (e != hipSuccess) return hip_fail(e, "merge launch");
     return VA_OK;
@@ -186,7 +209,7 @@ int va_decode(va_fmt fmt, const va_bufs* b, int H, int L, int D, int G, int S, v
 int va_decode_splits(va_fmt fmt, const va_bufs* b, int H, int L, int D, int G, int S, void* stream) {
     const int rc = validate(fmt, b, H, L, D, G, S, false);
     if (rc) return rc;
-    return run_splits(fmt, b, H, L, D, G, S, stream, false);
+    return run_splits(fmt, b, H, L, D, G, S, stream, -1);
 }
 
 int va_merge(const float* ws, uint16_t* out, int H, int D, int S, void* stream) {
@@ -195,6 +218,30 @@ int va_merge(const float* ws, uint16_t* out, int H, int D, int S, void* stream) 
     if (!aligned(ws, 4) || !aligned(out, 2)) return fail(VA_EALIGN, "ws/out misaligned");
     const hipError_t e = va::launch_merge(ws, out, H, D, S, as_stream(stream));
     if (e != hipSuccess) return hip_fail(e, "merge launch");
+    return VA_OK;
+}
+
+// Fused merges that gave up waiting for a partial, per device, as last reported
+// (the device counters only grow; the difference is what is new).
+unsigned g_lost_seen[64];
+std::mutex g_lost_mu;
+
+int va_merge_faults(void* stream, unsigned* count) {
+    if (!count) return fail(VA_ENULL, "count is NULL");
+    *count = 0;
+    int dev = 0;
+    VA_HIP(hipGetDevice(&dev), "hipGetDevice");
+    if (dev < 0 || dev >= 64) return fail(VA_ENODEV, "device index %d out of range", dev);
+    VA_HIP(hipStreamSynchronize(as_stream(stream)), "hipStreamSynchronize");
+    unsigned n1 = 0, n2 = 0;
+    VA_HIP(va::lost_merges_decode(&n1), "lost-merge counter");
+    VA_HIP(va::lost_merges_ex(&n2), "lost-merge counter");
+    std::lock_guard<std::mutex> lock(g_lost_mu);
+    const unsigned total = n1 + n2;
+    *count = total - g_lost_seen[dev];
+    g_lost_seen[dev] = total;
+    if (*count)
+        return fail(VA_ELOST, "%u fused merge(s) gave up waiting for a partial (their outputs are NaN)", *count);
     return VA_OK;
 }
 
@@ -242,8 +289,8 @@ bool fused_ok(int groups, int qg, int S) {
 
 int launch_ex(va_fmt fmt, va::DecodeArgs& a, int D, int G, int qg, bool paged, int groups,
               int heads_total, void* stream) {
-    const bool fused = fused_ok(groups, qg, a.S);
-    a.ticket_slot = fused ? (int)(g_ticket_seq.fetch_add(1u) % va::TICKET_SLOTS) : -1;
+    a.ticket_slot = fused_ok(groups, qg, a.S) ? ticket_slot_for(stream) : -1;
+    const bool fused = a.ticket_slot >= 0;
     a.qscale = (float)(1.4426950408889634074 / std::sqrt((double)D));
     hipError_t e = va::launch_decode_ex(kind_of(fmt), D, is_f16(fmt) ? 64 : G, qg, paged, groups, a,
                                         as_stream(stream));
@@ -604,6 +651,11 @@ int va_stream_create(void** stream) {
     return VA_OK;
 }
 int va_stream_destroy(void* stream) {
+    // The stream's ticket slot is freed once its last call has finished.
+    VA_HIP(hipStreamSynchronize(as_stream(stream)), "hipStreamSynchronize");
+    int dev = 0;
+    VA_HIP(hipGetDevice(&dev), "hipGetDevice");
+    g_slots.release(dev, reinterpret_cast<uintptr_t>(stream), 0);
     VA_HIP(hipStreamDestroy(as_stream(stream)), "hipStreamDestroy");
     return VA_OK;
 }
@@ -645,12 +697,22 @@ int va_graph_begin(void* stream) {
 }
 int va_graph_end(void* stream, void** graph_exec) {
     if (!stream || !graph_exec) return fail(VA_ENULL, "stream and graph_exec must be non-NULL");
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    unsigned long long id = 0;
+    VA_HIP(hipStreamGetCaptureInfo(as_stream(stream), &cs, &id), "hipStreamGetCaptureInfo");
     hipGraph_t g = nullptr;
     VA_HIP(hipStreamEndCapture(as_stream(stream), &g), "hipStreamEndCapture");
     hipGraphExec_t x = nullptr;
     const hipError_t e = hipGraphInstantiate(&x, g, nullptr, nullptr, 0);
     (void)hipGraphDestroy(g);
-    if (e != hipSuccess) return hip_fail(e, "hipGraphInstantiate");
+    if (e != hipSuccess) {
+        if (cs == hipStreamCaptureStatusActive) g_slots.release_capture(id | (1ull << 63));
+        return hip_fail(e, "hipGraphInstantiate");
+    }
+    if (cs == hipStreamCaptureStatusActive) {
+        std::lock_guard<std::mutex> lock(g_graph_mu);
+        g_graph_capture[x] = id | (1ull << 63);
+    }
     *graph_exec = x;
     return VA_OK;
 }
@@ -659,7 +721,19 @@ int va_graph_launch(void* graph_exec, void* stream) {
     return VA_OK;
 }
 int va_graph_destroy(void* graph_exec) {
+    // The ticket slots the capture bound are freed once no replay is running.
+    unsigned long long capture = 0;
+    {
+        std::lock_guard<std::mutex> lock(g_graph_mu);
+        auto it = g_graph_capture.find(graph_exec);
+        if (it != g_graph_capture.end()) {
+            capture = it->second;
+            g_graph_capture.erase(it);
+        }
+    }
+    if (capture) VA_HIP(hipDeviceSynchronize(), "hipDeviceSynchronize");
     VA_HIP(hipGraphExecDestroy(static_cast<hipGraphExec_t>(graph_exec)), "hipGraphExecDestroy");
+    g_slots.release_capture(capture);
     return VA_OK;
 }
 

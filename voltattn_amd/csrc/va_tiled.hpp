@@ -101,8 +101,7 @@ __global__ __launch_bounds__(WAVES * 64, MINB) void decode_tiled(DecodeArgs a) {
     if constexpr (PAGED) {
         const int cap = min(a.L, min(a.S * a.chunk, a.max_pages << a.page_shift));
         L = a.seq_lens[b];
-        if (L > cap) { bad = true; L = cap; }
-        L = max(L, 0);
+        if (L > cap || L < 0) { bad = true; L = L < 0 ? 0 : cap; }   // outside [0, max_seq_len]: NaN output
     }
     const int j0 = s * a.chunk;
     const int n  = min(L - j0, a.chunk);         // rows of this split (<= 0: empty)

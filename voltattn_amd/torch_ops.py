@@ -13,9 +13,12 @@ Importing this module registers
 Tensors keep the C ABI's layouts (include/voltattn.h): q/out fp16 [.., H, D];
 quantized K/V payload uint8 [.., L, row bytes]; f16 K/V fp16 [.., L, D]; scales
 fp16 [.., L, D/G]. Every op runs asynchronously on torch's current HIP stream
-and fails loudly (RuntimeError with the library's message) on invalid input;
-there is no CPU fallback: the tensors must live on a gfx950 device. Each op has
-a fake (meta) implementation, so shapes propagate under torch.compile.
+and fails loudly on invalid input: the shapes and dtypes of every tensor are
+checked against (fmt, D, G) before the C ABI is called, in the real and the
+fake (meta) implementation alike (RuntimeError), and the library's own checks
+raise with its message. There is no CPU fallback: the tensors must live on a
+gfx950 device. Each op has a fake implementation, so shapes propagate under
+torch.compile.
 """
 from __future__ import annotations
 
@@ -24,7 +27,7 @@ from typing import Optional
 
 import torch
 
-from . import (Fmt, _Bufs, _PagedBufs, _PagedShape, check, fmt_bits, lib, ws_bytes)
+from . import (Fmt, _Bufs, _PagedBufs, _PagedShape, check, fmt_bits, lib, row_bytes, ws_bytes)
 
 __all__ = ["decode", "decode_gqa", "decode_paged", "append_kv", "quantize"]
 
@@ -53,12 +56,117 @@ def _D_of(q: torch.Tensor) -> int:
     return int(q.shape[-1])
 
 
+def _fail(msg: str):
+    raise RuntimeError(f"voltattn: {msg}")
+
+
+def _expect(t: torch.Tensor, name: str, shape: tuple, dtype: torch.dtype) -> None:
+    if t is None:
+        _fail(f"{name} is required")
+    if tuple(int(x) for x in t.shape) != tuple(shape):
+        _fail(f"{name} has shape {tuple(t.shape)}, expected {tuple(shape)}")
+    if t.dtype != dtype:
+        _fail(f"{name} has dtype {t.dtype}, expected {dtype}")
+
+
+def _check_dg(f: Fmt, D: int, group: int) -> None:
+    if D not in (64, 128):
+        _fail(f"D must be 64 or 128 (got {D})")
+    if fmt_bits(f) != 16 and not (group in (32, 64) and group <= D):
+        _fail(f"group must be 32 or 64 and <= D (got {group}, D={D})")
+
+
+def _row_shape(f: Fmt, D: int) -> tuple[tuple, torch.dtype]:
+    """Trailing shape and dtype of one K/V row of format f: fp16 [D] for the f16
+    formats, uint8 [row bytes] for the quantized ones."""
+    if fmt_bits(f) == 16:
+        return (D,), torch.float16
+    return (row_bytes(f, D),), torch.uint8
+
+
+def _check_kv(f: Fmt, k, v, ks, vs, lead: tuple, D: int, group: int) -> None:
+    """k, v [*lead, row]; scales fp16 [*lead, D/G] for quantized formats."""
+    tail, dt = _row_shape(f, D)
+    _expect(k, "k", lead + tail, dt)
+    _expect(v, "v", lead + tail, dt)
+    if fmt_bits(f) != 16:
+        _expect(ks, "k_scale", lead + (D // group,), torch.float16)
+        _expect(vs, "v_scale", lead + (D // group,), torch.float16)
+
+
+def _validate_decode(q, k, v, ks, vs, f: Fmt, group: int, grouped: bool) -> None:
+    if q.dim() != 2:
+        _fail(f"q must be [H, D] (got {tuple(q.shape)})")
+    H, D = (int(x) for x in q.shape)
+    _expect(q, "q", (H, D), torch.float16)
+    _check_dg(f, D, group)
+    if k.dim() != 3:
+        _fail(f"k must be [heads, L, row] (got {tuple(k.shape)})")
+    Hk, L = int(k.shape[0]), int(k.shape[1])
+    if grouped:
+        if Hk < 1 or H % Hk:
+            _fail(f"query heads ({H}) must be a multiple of K/V heads ({Hk})")
+    elif Hk != H:
+        _fail(f"k has {Hk} heads, q has {H}")
+    _check_kv(f, k, v, ks, vs, (Hk, L), D, group)
+
+
+def _validate_paged(q, kp, vp, ksp, vsp, block_table, seq_lens, f: Fmt, group: int) -> None:
+    if q.dim() != 3:
+        _fail(f"q must be [B, Hq, D] (got {tuple(q.shape)})")
+    B, Hq, D = (int(x) for x in q.shape)
+    _expect(q, "q", (B, Hq, D), torch.float16)
+    _check_dg(f, D, group)
+    if kp.dim() != 4:
+        _fail(f"k_pages must be [num_pages, Hkv, page_rows, row] (got {tuple(kp.shape)})")
+    num_pages, Hkv, page_rows = (int(x) for x in kp.shape[:3])
+    if Hkv < 1 or Hq % Hkv:
+        _fail(f"query heads ({Hq}) must be a multiple of K/V heads ({Hkv})")
+    _check_kv(f, kp, vp, ksp, vsp, (num_pages, Hkv, page_rows), D, group)
+    if block_table.dim() != 2 or int(block_table.shape[0]) != B:
+        _fail(f"block_table must be [B={B}, max_pages] (got {tuple(block_table.shape)})")
+    _expect(block_table, "block_table", (B, int(block_table.shape[1])), torch.int32)
+    _expect(seq_lens, "seq_lens", (B,), torch.int32)
+
+
+def _validate_append(x, start, block_table, pages, scale_pages, f: Fmt, group: int) -> None:
+    if x.dim() != 4:
+        _fail(f"x must be [B, Hkv, n, D] (got {tuple(x.shape)})")
+    B, Hkv, n, D = (int(s) for s in x.shape)
+    _expect(x, "x", (B, Hkv, n, D), torch.float16)
+    _check_dg(f, D, group)
+    if pages.dim() != 4:
+        _fail(f"pages must be [num_pages, Hkv, page_rows, row] (got {tuple(pages.shape)})")
+    num_pages, Hp, page_rows = (int(s) for s in pages.shape[:3])
+    if Hp != Hkv:
+        _fail(f"pages hold {Hp} K/V heads, x has {Hkv}")
+    tail, dt = _row_shape(f, D)
+    _expect(pages, "pages", (num_pages, Hkv, page_rows) + tail, dt)
+    if fmt_bits(f) != 16:
+        _expect(scale_pages, "scale_pages", (num_pages, Hkv, page_rows, D // group), torch.float16)
+    _expect(start, "start", (B,), torch.int32)
+    if block_table.dim() != 2 or int(block_table.shape[0]) != B:
+        _fail(f"block_table must be [B={B}, max_pages] (got {tuple(block_table.shape)})")
+    _expect(block_table, "block_table", (B, int(block_table.shape[1])), torch.int32)
+
+
+def _validate_quantize(x, bits: int, group: int) -> None:
+    if bits not in (8, 4, 3):
+        _fail(f"bits must be 8, 4 or 3 (got {bits})")
+    if x.dtype != torch.float32:
+        _fail(f"x must be fp32 (got {x.dtype})")
+    D = int(x.shape[-1]) if x.dim() else 0
+    if not (group in (32, 64) and D >= group and D % group == 0 and D % 8 == 0):
+        _fail(f"group must be 32 or 64 and divide D (got group={group}, D={D})")
+
+
 @torch.library.custom_op("voltattn::decode", mutates_args=())
 def decode(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, k_scale: Optional[torch.Tensor],
            v_scale: Optional[torch.Tensor], fmt: str, group: int = 32, splits: int = 0) -> torch.Tensor:
     """q fp16 [H, D]; k, v [H, L, row] (uint8) or [H, L, D] (fp16 formats); scales fp16 [H, L, D/G]."""
-    _need_gpu(q, k, v, k_scale, v_scale)
     f = _fmt(fmt)
+    _validate_decode(q, k, v, k_scale, v_scale, f, group, grouped=False)
+    _need_gpu(q, k, v, k_scale, v_scale)
     H, D, L = int(q.shape[0]), _D_of(q), int(k.shape[1])
     S = splits
     if S <= 0:
@@ -74,6 +182,7 @@ def decode(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, k_scale: Optional[
 
 @decode.register_fake
 def _(q, k, v, k_scale, v_scale, fmt, group=32, splits=0):
+    _validate_decode(q, k, v, k_scale, v_scale, _fmt(fmt), group, grouped=False)
     return q.new_empty((q.shape[0], q.shape[-1]), dtype=torch.float16)
 
 
@@ -81,8 +190,9 @@ def _(q, k, v, k_scale, v_scale, fmt, group=32, splits=0):
 def decode_gqa(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, k_scale: Optional[torch.Tensor],
                v_scale: Optional[torch.Tensor], fmt: str, group: int = 32, splits: int = 0) -> torch.Tensor:
     """q fp16 [Hq, D]; k, v [Hkv, L, ...]; query head h attends KV head h // (Hq / Hkv)."""
-    _need_gpu(q, k, v, k_scale, v_scale)
     f = _fmt(fmt)
+    _validate_decode(q, k, v, k_scale, v_scale, f, group, grouped=True)
+    _need_gpu(q, k, v, k_scale, v_scale)
     Hq, Hkv, D, L = int(q.shape[0]), int(k.shape[0]), _D_of(q), int(k.shape[1])
     S = splits
     if S <= 0:
@@ -98,6 +208,7 @@ def decode_gqa(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, k_scale: Optio
 
 @decode_gqa.register_fake
 def _(q, k, v, k_scale, v_scale, fmt, group=32, splits=0):
+    _validate_decode(q, k, v, k_scale, v_scale, _fmt(fmt), group, grouped=True)
     return q.new_empty((q.shape[0], q.shape[-1]), dtype=torch.float16)
 
 
@@ -115,10 +226,9 @@ def decode_paged(q: torch.Tensor, k_pages: torch.Tensor, v_pages: torch.Tensor,
                  group: int = 32, splits: int = 0) -> torch.Tensor:
     """q fp16 [B, Hq, D]; pages [num_pages, Hkv, page_rows, ...]; block_table int32
     [B, max_pages]; seq_lens int32 [B] (each <= max_seq_len)."""
-    _need_gpu(q, k_pages, v_pages, k_scale_pages, v_scale_pages, block_table, seq_lens)
-    if block_table.dtype != torch.int32 or seq_lens.dtype != torch.int32:
-        raise RuntimeError("block_table and seq_lens must be int32")
     f = _fmt(fmt)
+    _validate_paged(q, k_pages, v_pages, k_scale_pages, v_scale_pages, block_table, seq_lens, f, group)
+    _need_gpu(q, k_pages, v_pages, k_scale_pages, v_scale_pages, block_table, seq_lens)
     shape = _paged_shape(q, k_pages, block_table, group, max_seq_len)
     S = splits
     if S <= 0:
@@ -137,6 +247,7 @@ def decode_paged(q: torch.Tensor, k_pages: torch.Tensor, v_pages: torch.Tensor,
 @decode_paged.register_fake
 def _(q, k_pages, v_pages, k_scale_pages, v_scale_pages, block_table, seq_lens, fmt, max_seq_len,
       group=32, splits=0):
+    _validate_paged(q, k_pages, v_pages, k_scale_pages, v_scale_pages, block_table, seq_lens, _fmt(fmt), group)
     return q.new_empty(q.shape, dtype=torch.float16)
 
 
@@ -145,10 +256,9 @@ def append_kv(x: torch.Tensor, start: torch.Tensor, block_table: torch.Tensor, p
               scale_pages: Optional[torch.Tensor], fmt: str, group: int = 32) -> None:
     """x fp16 [B, Hkv, n, D] new rows written at positions start[b] + r of the paged cache
     pages [num_pages, Hkv, page_rows, ...] (+ scale_pages for quantized formats)."""
-    _need_gpu(x, start, block_table, pages, scale_pages)
-    if x.dtype != torch.float16:
-        raise RuntimeError("x must be fp16")
     f = _fmt(fmt)
+    _validate_append(x, start, block_table, pages, scale_pages, f, group)
+    _need_gpu(x, start, block_table, pages, scale_pages)
     B, Hkv, n, D = (int(s) for s in x.shape)
     num_pages, _, page_rows = (int(s) for s in pages.shape[:3])
     shape = _PagedShape(B, Hkv, Hkv, D, group, page_rows, int(block_table.shape[1]), num_pages, 0)
@@ -158,15 +268,15 @@ def append_kv(x: torch.Tensor, start: torch.Tensor, block_table: torch.Tensor, p
 
 @append_kv.register_fake
 def _(x, start, block_table, pages, scale_pages, fmt, group=32):
+    _validate_append(x, start, block_table, pages, scale_pages, _fmt(fmt), group)
     return None
 
 
 @torch.library.custom_op("voltattn::quantize", mutates_args=())
 def quantize(x: torch.Tensor, bits: int, group: int = 32) -> tuple[torch.Tensor, torch.Tensor]:
     """x fp32 [..., D] -> (packed uint8 [..., D*bits/8], fp16 scales [..., D/G])."""
+    _validate_quantize(x, bits, group)
     _need_gpu(x)
-    if x.dtype != torch.float32:
-        raise RuntimeError("x must be fp32")
     D = int(x.shape[-1])
     rows = x.numel() // D
     packed = torch.empty(x.shape[:-1] + (D * bits // 8,), dtype=torch.uint8, device=x.device)
@@ -177,6 +287,7 @@ def quantize(x: torch.Tensor, bits: int, group: int = 32) -> tuple[torch.Tensor,
 
 @quantize.register_fake
 def _(x, bits, group=32):
+    _validate_quantize(x, bits, group)
     D = x.shape[-1]
     return (x.new_empty(x.shape[:-1] + (D * bits // 8,), dtype=torch.uint8),
             x.new_empty(x.shape[:-1] + (D // group,), dtype=torch.float16))
