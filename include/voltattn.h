@@ -91,6 +91,17 @@ typedef struct {
  * the partials go to ws and a separate merge kernel follows. */
 int va_decode(va_fmt fmt, const va_bufs* b, int H, int L, int D, int G, int S, void* stream);
 
+/* va_decode without a workspace argument, for callers that cannot allocate
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc). No counterpart in the reference. b->ws is ignored: the two-pass
+ * form's partials go to a workspace of library device memory (4 MiB per
+ * device, held until the process ends), so H*S*(D+2) must not exceed
+ * VA_NOALLOC_MAX_FLOATS (VA_ERANGE otherwise). Allocates nothing; same
+ * kernels and outputs as va_decode. Every call on a device shares that
+ * device's workspace: calls that overlap on one device race. */
+#define VA_NOALLOC_MAX_FLOATS 1048576
+int va_decode_noalloc(va_fmt fmt, const va_bufs* b, int H, int L, int D, int G, int S, void* stream);
+
 /* Fused merges on the current device that gave up waiting for a partial
  * (bounded poll exhausted; the affected outputs were set to NaN) since the
  * previous call. Synchronizes `stream` first. Returns VA_ELOST with *count > 0

@@ -95,6 +95,7 @@ _sig("va_decode", _I, _I, C.POINTER(_Bufs), _I, _I, _I, _I, _I, _P)
 _sig("va_decode_splits", _I, _I, C.POINTER(_Bufs), _I, _I, _I, _I, _I, _P)
 _sig("va_merge", _I, _P, _P, _I, _I, _I, _P)
 _sig("va_merge_faults", _I, _P, C.POINTER(C.c_uint))
+_sig("va_decode_noalloc", _I, _I, C.POINTER(_Bufs), _I, _I, _I, _I, _I, _P)
 _sig("va_ws_bytes", _SZ, _I, _I, _I)
 _sig("va_payload_bytes", _SZ, _I, _I, _I, _I)
 _sig("va_scale_bytes", _SZ, _I, _I, _I, _I, _I)

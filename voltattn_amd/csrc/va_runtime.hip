@@ -57,7 +57,8 @@ size_t row_bytes(va_fmt f, int D) { return (size_t)D * bits_of(f) / 8; }
 
 bool aligned(const void* p, size_t a) { return ((uintptr_t)p % a) == 0; }
 
-int validate(va_fmt fmt, const va_bufs* b, int H, int L, int D, int G, int S, bool need_out) {
+int validate(va_fmt fmt, const va_bufs* b, int H, int L, int D, int G, int S, bool need_out,
+             bool need_ws = true) {
     if (!valid_fmt(fmt)) return fail(VA_EINVAL, "invalid format %d", (int)fmt);
     if (!b) return fail(VA_ENULL, "bufs is NULL");
     if (D != 64 && D != 128) return fail(VA_EINVAL, "D must be 64 or 128 (got %d)", D);
@@ -70,14 +71,15 @@ int validate(va_fmt fmt, const va_bufs* b, int H, int L, int D, int G, int S, bo
     if ((long long)H * S > 0x7FFFFFFFLL) return fail(VA_ERANGE, "H*S too large");
     if (((size_t)L + 256) * row_bytes(fmt, D) >= 0x7FFFFFFFull)
         return fail(VA_ERANGE, "L*row bytes must stay below 2^31 (L=%d)", L);
-    if (!b->k || !b->v || !b->q || !b->ws) return fail(VA_ENULL, "k, v, q and ws must be non-NULL");
+    if (!b->k || !b->v || !b->q) return fail(VA_ENULL, "k, v and q must be non-NULL");
+    if (need_ws && !b->ws) return fail(VA_ENULL, "ws must be non-NULL");
     if (need_out && !b->out) return fail(VA_ENULL, "out must be non-NULL");
     if (quant && (!b->sk || !b->sv)) return fail(VA_ENULL, "quantized formats need sk and sv");
     const size_t kal = kind_of(fmt) == 3 ? 4 : 16;
     if (!aligned(b->k, kal) || !aligned(b->v, kal))
         return fail(VA_EALIGN, "k and v must be %zu-byte aligned", kal);
     if (!aligned(b->q, 16)) return fail(VA_EALIGN, "q must be 16-byte aligned");
-    if (!aligned(b->ws, 4)) return fail(VA_EALIGN, "ws must be 4-byte aligned");
+    if (need_ws && !aligned(b->ws, 4)) return fail(VA_EALIGN, "ws must be 4-byte aligned");
     if (need_out && !aligned(b->out, 2)) return fail(VA_EALIGN, "out must be 2-byte aligned");
     if (quant) {
         const size_t sal = (D / G) >= 2 ? 4 : 2;
@@ -202,6 +204,64 @@ int va_decode(va_fmt fmt, const va_bufs* b, int H, int L, int D, int G, int S, v
     rc = run_splits(fmt, b, H, L, D, G, S, stream, slot);
     if (rc || slot >= 0) return rc;
     const hipError_t e = va::launch_merge(b->ws, b->out, H, D, S, as_stream(stream));
+    if (e != hipSuccess) return hip_fail(e, "merge launch");
+    return VA_OK;
+}
+
+} // extern "C"
+
+// ------------------------------------------------ allocation-free decode --
+// Workspace of va_decode_noalloc: the two-pass form's partials (H*S*(D+2)
+// floats) live in this file-scope device array instead of a caller-provided
+// ws. Each device holds its own copy for the life of the process. Host code
+// never uses the array's name as an address: the per-device address comes
+// from hipGetSymbolAddress on the device's first call.
+namespace {
+
+constexpr size_t SCRATCH_FLOATS = VA_NOALLOC_MAX_FLOATS;   // 4 MiB: H*S*(D+2) <= 1,048,576
+static __device__ __align__(256) float scratch[SCRATCH_FLOATS];
+
+constexpr int SCRATCH_DEVICES = 64;
+float* g_scratch_ptr[SCRATCH_DEVICES];
+std::mutex g_scratch_mu;
+
+// This device's address of `scratch` (looked up once per device, with the
+// device current), or nullptr with the failure recorded.
+float* scratch_ptr(int* rc) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) { *rc = hip_fail(e, "hipGetDevice"); return nullptr; }
+    if (dev < 0 || dev >= SCRATCH_DEVICES) { *rc = fail(VA_ENODEV, "device index %d out of range", dev); return nullptr; }
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+        void* p = nullptr;
+        e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess) { *rc = hip_fail(e, "hipGetSymbolAddress(scratch)"); return nullptr; }
+        g_scratch_ptr[dev] = static_cast<float*>(p);
+    }
+    return g_scratch_ptr[dev];
+}
+
+} // namespace
+
+extern "C" {
+
+int va_decode_noalloc(va_fmt fmt, const va_bufs* b, int H, int L, int D, int G, int S, void* stream) {
+    if (!b) return fail(VA_ENULL, "bufs is NULL");
+    if (H >= 1 && S >= 1 && (D == 64 || D == 128) &&
+        (unsigned long long)H * S * (D + 2) > SCRATCH_FLOATS)
+        return fail(VA_ERANGE, "H*S*(D+2) = %llu floats exceeds the allocation-free workspace (%zu floats)",
+                    (unsigned long long)H * S * (D + 2), SCRATCH_FLOATS);
+    int rc = validate(fmt, b, H, L, D, G, S, true, false);
+    if (rc) return rc;
+    va_bufs nb = *b;
+    nb.ws = scratch_ptr(&rc);
+    if (!nb.ws) return rc;
+    const bool fits = H <= va::TICKET_MAXH && S <= 64 && (long long)H * S <= va::PART_CAP;
+    const int slot = fits ? ticket_slot_for(stream) : -1;
+    rc = run_splits(fmt, &nb, H, L, D, G, S, stream, slot);
+    if (rc || slot >= 0) return rc;
+    const hipError_t e = va::launch_merge(nb.ws, nb.out, H, D, S, as_stream(stream));
     if (e != hipSuccess) return hip_fail(e, "merge launch");
     return VA_OK;
 }
