@@ -1,16 +1,18 @@
 #!/usr/bin/env python3
 """Benchmark of the fused dequant + decode-attention path on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--L 16384] [--G 32]
+    python bench.py [--gpus 1] [--steps K] [--warmup W]
 
 One "step" is one decode step: one query token attending over L cached
 positions for all H=32 heads (D=128), i.e. one va_decode() call (split-L
-attention pass + log-sum-exp merge pass), reading a compressed K/V cache that is
+attention pass + log-sum-exp merge), reading a compressed K/V cache that is
 already resident in HBM. The headline workload is BASELINE.json's metric at
 H=32 D=128 L=16384 with G=32 scales; `value` is the q8+ (fused INT8) decode
-rate in tok/s. f16, f16+ and q4+ at the same shape are reported in
-`formats`, each with ms, GB/s, MBU against the probed read ceiling, % of the
-8 TB/s peak, and tok/s.
+rate in tok/s. Every BASELINE config is measured in the same run (`configs`):
+q8/q8+ at L=4096, f16/f16+ at 16384 ([1]), q8+ at 16384 and
+65536 ([2]), q4+ at 4096, 16384 and 65536 ([3]), q3+ at 65536 and 262144 ([4]),
+each with ms, GB/s, MBU against the probed read ceiling, % of the 8 TB/s peak
+and tok/s; `formats` repeats the L=16384 rows by format.
 
 Method (reference bench, src/voltattn.cu:967-1070, re-derived for MI355X):
   * read ceiling: a >= 4 GiB buffer (16x the 256 MB Infinity Cache) read with
@@ -18,18 +20,24 @@ Method (reference bench, src/voltattn.cu:967-1070, re-derived for MI355X):
   * K/V are drawn N(0,1) on the GPU, quantized there (bit-exact quantizer) and
     replicated into enough copies to rotate a >= 2 GiB working set, so the
     MALL cannot serve the stream;
-  * timed region: K back-to-back steps between two HIP events on the launch
-    stream, bracketed by device synchronisation -> ms_per_step (the value);
-    plus the reference's best-of-K single-launch time, each launch preceded by
-    an untimed one so the start event is stamped when the GPU is already busy;
+  * timed region: device synchronisation, one untimed lead step (so the start
+    event is stamped while the GPU is busy and the host's latency to enqueue
+    the first timed step is not counted), then K back-to-back steps between two
+    HIP events on the launch stream, then synchronisation -> ms_per_step; plus
+    the reference's best-of-K single launch, each behind an untimed lead step;
+  * correctness: after timing, every row's output (the last timed step; all
+    copies hold the same data) is gated head by head against the oracle's
+    double reference over the downloaded packed bytes (the reference gates its
+    bench on its selftest, src/voltattn.cu:1075-1076); `checked` is true only
+    if every row passes, and the process exits non-zero otherwise;
   * roofline: algorithmic bytes per decode-kernel launch (compressed K+V
     payload + fp16 scales: 2*H*L*(D*b/8 + 2*D/G)) over the fused decode
     kernel's mean launch time (the K back-to-back steps between events: one
-    launch per step); the split pass alone (va_decode_splits, K back-to-back
-    launches) is reported beside it;
+    launch per step); the split pass alone (va_decode_splits) beside it;
   * cpu_baseline: the oracle's double-precision reference attention
-    (reference(), src/voltattn.cu:769-794) over the same shape, timed on this
-    host (rank 0, N=1 only).
+    (reference(), src/voltattn.cu:769-794) on the headline shape, timed on
+    this host (rank 0, N=1 only); `cpu_configs0` is the same on configs[0]
+    (q8, L=4096), at 1 core and at T cores, with nproc and the CPU model.
 """
 from __future__ import annotations
 
@@ -143,8 +151,11 @@ def time_workload(va, w: Workload, steps: int, warmup: int, stream) -> dict:
         for i in range(warmup):
             launch(i)
         va.sync()
-        # (1) K back-to-back steps, rotating copies: the contract's timed region
-        va.sync()
+        # (1) the contract's timed region: K back-to-back steps, rotating copies,
+        # between two events on the launch stream. One untimed lead step goes
+        # first, so the start event is stamped while the GPU is busy and the
+        # host's latency to enqueue the first timed step is not counted.
+        launch(steps)
         e0.record(stream)
         for i in range(steps):
             launch(i)
@@ -161,17 +172,51 @@ def time_workload(va, w: Workload, steps: int, warmup: int, stream) -> dict:
             e1.record(stream)
             e1.synchronize()
             best_ms = min(best_ms, e0.elapsed_ms(e1))
-        # (3) first pass alone, back-to-back: the decode kernel's mean launch time
+        # (3) first pass alone, back-to-back: the split pass's mean launch time
+        first(steps)
         e0.record(stream)
         for i in range(steps):
             first(i)
         e1.record(stream)
         e1.synchronize()
         kern_ms = e0.elapsed_ms(e1) / steps
+        # the output checked below is that of one full step
+        launch(0)
+        va.sync()
     finally:
         e0.destroy()
         e1.destroy()
     return {"mean_ms": mean_ms, "best_ms": best_ms, "kernel_ms": kern_ms}
+
+
+def check_workload(va, w: Workload, heads) -> dict:
+    """Checker (not timed): the last step's fp16 output against the oracle's
+    double reference attention over copy 0's packed bytes (all copies are
+    equal), head by head: the reference's gate |got-ref| <= 3e-3 + 2e-2|ref|
+    (src/voltattn.cu:903) and the fp16 rounding bound of tests/numerics.py."""
+    import numpy as np
+    import oracle
+    from tests.numerics import tight_bound
+    H, L, D, G, fmt = w.H, w.L, w.D, w.G, w.fmt
+    bits = va.fmt_bits(fmt)
+    out = w.out.download(np.uint16).view(np.float16).astype(np.float64).reshape(H, D)
+    q = w.q.download(np.uint16).reshape(H, D)
+    row = w.pay // (H * L)
+    ns = L * D // G
+    worst, ok = 0.0, bool(np.all(np.isfinite(out)))
+    for h in heads:
+        kp = w.K.download(np.uint8, L * row, offset=h * L * row)
+        vp = w.V.download(np.uint8, L * row, offset=h * L * row)
+        if bits == 16:
+            kd, vd = kp.view(np.float16).astype(np.float32), vp.view(np.float16).astype(np.float32)
+        else:
+            kd = oracle.dequant(kp, w.SK.download(np.uint16, ns, offset=h * ns * 2), L, D, G, bits)
+            vd = oracle.dequant(vp, w.SV.download(np.uint16, ns, offset=h * ns * 2), L, D, G, bits)
+        ref = oracle.reference(kd, vd, q[h], 1, L, D).astype(np.float64)
+        gate_ok, maxerr = oracle.gate(out[h], ref)
+        ok = ok and gate_ok and bool(np.all(np.abs(out[h] - ref) <= tight_bound(ref)))
+        worst = max(worst, maxerr)
+    return {"checked": ok, "check_heads": list(heads), "check_maxerr": worst}
 
 
 def time_fn(va, fn, copies: int, steps: int, warmup: int, stream) -> float:
@@ -183,6 +228,7 @@ def time_fn(va, fn, copies: int, steps: int, warmup: int, stream) -> float:
         for i in range(warmup):
             fn(i % copies, stream)
         va.sync()
+        fn(steps % copies, stream)          # untimed lead step: the start event is stamped while busy
         e0.record(stream)
         for i in range(steps):
             fn(i % copies, stream)
@@ -282,34 +328,62 @@ def bench_paged(va, fmt, B, Hq, Hkv, L, P, D, G, steps, warmup, stream, min_set)
             b.free()
 
 
-def cpu_baseline(H, L, D, G) -> dict:
-    """The oracle's reference() on one full decode step of the workload (q8 inputs)."""
+def _cpu_model() -> str:
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def cpu_reference(H, L, D, G, seconds=2.0) -> dict:
+    """The oracle's double-precision reference() (src/voltattn.cu:769-794) on one
+    full decode step of q8 inputs (dequantized K/V, format-independent work:
+    2*H*L*D MACs), timed on this host: repeated for about `seconds` per line,
+    single thread and heads split over T threads; mean and best."""
     import numpy as np
     import oracle
     t0 = time.time()
     c = oracle.make_case(8, H, L, D, G, 0x1234 + L)
     prep_s = time.time() - t0
     kd, vd, q = c["kd"], c["vd"], c["q"]
-    best = float("inf")
-    for _ in range(3):
-        t = time.perf_counter()
-        out = oracle.reference(kd, vd, q, H, L, D)
-        best = min(best, time.perf_counter() - t)
     threads = max(1, min(H, 16, os.cpu_count() or 1))
-    best_mt = float("inf")
-    for _ in range(3):
-        t = time.perf_counter()
-        out_mt = oracle.reference(kd, vd, q, H, L, D, threads=threads)
-        best_mt = min(best_mt, time.perf_counter() - t)
-    assert np.array_equal(out, out_mt)
+
+    def run(th):
+        times, out = [], None
+        t_end = time.perf_counter() + seconds
+        while not times or time.perf_counter() < t_end:
+            t = time.perf_counter()
+            out = oracle.reference(kd, vd, q, H, L, D, threads=th)
+            times.append(time.perf_counter() - t)
+        return out, times
+
+    out1, t1 = run(1)
+    outT, tT = run(threads)
+    assert np.array_equal(out1, outT)
+    mean1, meanT = sum(t1) / len(t1), sum(tT) / len(tT)
     return {
-        "value": 1.0 / best, "unit": "tok/s", "cores": 1, "kind": "port",
-        "sample": (f"one full decode step (q8, H={H} D={D} L={L} G={G}): double-precision "
-                   f"reference() over the dequantized K/V, best of 3 single-thread runs"),
-        "ms": best * 1e3,
-        "multithread": {"value": 1.0 / best_mt, "unit": "tok/s", "cores": threads,
-                        "ms": best_mt * 1e3},
-        "input_prep_s": prep_s,
+        "ms": mean1 * 1e3, "best_ms": min(t1) * 1e3, "runs": len(t1), "tok_s": 1.0 / mean1,
+        "multithread": {"ms": meanT * 1e3, "best_ms": min(tT) * 1e3, "runs": len(tT),
+                        "tok_s": 1.0 / meanT, "cores": threads},
+        "nproc": os.cpu_count(), "cpu_model": _cpu_model(), "input_prep_s": prep_s,
+        "shape": f"q8 H={H} D={D} L={L} G={G}",
+    }
+
+
+def cpu_baseline(H, L, D, G) -> dict:
+    """The contract's cpu_baseline: the headline shape on the oracle, 1 core."""
+    r = cpu_reference(H, L, D, G, seconds=6.0)
+    return {
+        "value": r["tok_s"], "unit": "tok/s", "cores": 1, "kind": "port",
+        "sample": (f"full decode steps ({r['shape']}): double-precision reference() over the "
+                   f"dequantized K/V, {r['runs']} single-thread runs (~6 s), mean"),
+        "ms": r["ms"], "best_ms": r["best_ms"],
+        "multithread": {"value": r["multithread"]["tok_s"], "unit": "tok/s",
+                        "cores": r["multithread"]["cores"], "ms": r["multithread"]["ms"]},
+        "nproc": r["nproc"], "cpu_model": r["cpu_model"], "input_prep_s": r["input_prep_s"],
     }
 
 
@@ -325,21 +399,34 @@ def load_traffic(name: str):
     return None if entry is None else float(entry["traffic_bytes"])
 
 
+# (config index, format, L); H=32, D=128, G=32.
+CONFIG_ROWS = [
+    (0, "q8", 4096), (0, "q8+", 4096),
+    (1, "f16", 16384), (1, "f16+", 16384),
+    (2, "q8+", 16384), (2, "q8+", 65536),
+    (3, "q4+", 4096), (3, "q4+", 16384), (3, "q4+", 65536),
+    (4, "q3+", 65536), (4, "q3+", 262144),
+    (None, "q3+", 16384),                       # q3+ at the metric's shape (not a BASELINE config)
+]
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--L", type=int, default=16384)
     ap.add_argument("--G", type=int, default=32)
     ap.add_argument("--H", type=int, default=32)
     ap.add_argument("--D", type=int, default=128)
-    ap.add_argument("--formats", default="f16,f16+,q8+,q4+")
     ap.add_argument("--headline", default="q8+")
+    ap.add_argument("--L", type=int, default=16384, help="the headline's L")
+    ap.add_argument("--rows", default="all",
+                    help="'all' (every BASELINE config) or a comma list of fmt:L, e.g. q8+:16384,f16+:16384")
     ap.add_argument("--splits", type=int, default=0, help="force S (0: va_pick_splits)")
     ap.add_argument("--probe-gib", type=float, default=4.0)
-    ap.add_argument("--set-gib", type=float, default=2.0, help="rotated working set per format")
+    ap.add_argument("--set-gib", type=float, default=2.0, help="rotated working set per row")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-check", action="store_true", help="skip the after-timing output check")
     ap.add_argument("--no-extra", action="store_true",
                     help="skip the grouped-query and paged workloads (reported under 'extra')")
     ap.add_argument("--copy-probe-mib", type=int, default=0,
@@ -375,32 +462,45 @@ def main() -> int:
             dst.free()
         log(f"copy probe: {nb} bytes device-to-device")
 
-    H, L, D, G = args.H, args.L, args.D, args.G
+    H, D, G = args.H, args.D, args.G
+    if args.rows == "all":
+        rows_spec = list(CONFIG_ROWS)
+    else:
+        rows_spec = [(None, x.split(":")[0], int(x.split(":")[1])) for x in args.rows.split(",") if x]
+    if not any(f == args.headline and L == args.L for _, f, L in rows_spec):
+        rows_spec.append((None, args.headline, args.L))
     stream = va.Stream()
-    rows = {}
-    for name in [s for s in args.formats.split(",") if s]:
+    rows = []
+    for cfg, name, L in rows_spec:
         fmt = va.Fmt.parse(name)
         w = Workload(va, fmt, H, L, D, G, int(args.set_gib * 2**30), 256)
         try:
             S = args.splits or va.pick_splits(fmt, H, L, D)
             w.set_splits(S)
             t = time_workload(va, w, args.steps, args.warmup, stream)
+            chk = {"checked": None} if args.no_check else check_workload(va, w, (0, H // 2, H - 1))
         finally:
             w.free()
         nbytes = algo_bytes(fmt, H, L, D, G)
         gbs = nbytes / (t["mean_ms"] * 1e6)
-        rows[fmt.label] = {
-            "ms": t["mean_ms"], "best_single_ms": t["best_ms"], "kernel_ms": t["kernel_ms"],
-            "tok_s": 1e3 / t["mean_ms"], "tok_s_best_single": 1e3 / t["best_ms"],
-            "bytes": nbytes, "gbps": gbs, "mbu": gbs / ceiling, "pct_peak": gbs / PEAK_HBM_GBPS,
-            "kernel_gbps": nbytes / (t["kernel_ms"] * 1e6),
-            "S": S, "copies": w.copies, "working_set_bytes": w.copies * w.copy_bytes,
-        }
-        r = rows[fmt.label]
-        log(f"{fmt.label:5s} L={L} G={G} S={S:3d} copies={w.copies:3d}  "
+        r = {"config": cfg, "fmt": fmt.label, "L": L, "S": S,
+             "ms": t["mean_ms"], "best_single_ms": t["best_ms"], "split_pass_ms": t["kernel_ms"],
+             "tok_s": 1e3 / t["mean_ms"], "tok_s_best_single": 1e3 / t["best_ms"],
+             "bytes": nbytes, "gbps": gbs, "mbu": gbs / ceiling, "pct_peak": gbs / PEAK_HBM_GBPS,
+             "copies": w.copies, "working_set_bytes": w.copies * w.copy_bytes, **chk}
+        rows.append(r)
+        log(f"cfg[{'-' if cfg is None else cfg}] {fmt.label:5s} L={L:6d} S={S:3d} copies={w.copies:3d}  "
             f"mean {r['ms'] * 1e3:8.2f} us  best {r['best_single_ms'] * 1e3:8.2f} us  "
-            f"kernel {r['kernel_ms'] * 1e3:8.2f} us  {gbs:7.1f} GB/s  MBU {100 * r['mbu']:5.1f}%  "
-            f"tok/s {r['tok_s']:8.0f}")
+            f"{gbs:7.1f} GB/s  MBU {100 * r['mbu']:5.1f}%  peak {100 * r['pct_peak']:5.1f}%  "
+            f"tok/s {r['tok_s']:8.0f}  check {'-' if r['checked'] is None else ('ok' if r['checked'] else 'FAIL')}")
+    # vs f16 / vs f16+ at the same L
+    for r in rows:
+        for ref_fmt, key in (("f16", "vs_f16"), ("f16+", "vs_f16p")):
+            base = [x for x in rows if x["fmt"] == ref_fmt and x["L"] == r["L"]]
+            if base:
+                r[key] = base[0]["ms"] / r["ms"]
+    formats = {r["fmt"]: r for r in rows if r["L"] == args.L}
+
     extra = {}
     if not args.no_extra:
         # Beyond the reference (grouped-query attention, paged batches): same bytes
@@ -427,49 +527,61 @@ def main() -> int:
             log(f"{key:48s} S={r['S']:3d}  mean {r['ms'] * 1e3:8.2f} us  {gbs:7.1f} GB/s  "
                 f"MBU {100 * gbs / ceiling:5.1f}%  tok/s {seqs * 1e3 / r['ms']:8.0f}")
     stream.destroy()
-    for r in rows.values():
-        if "f16" in rows:
-            r["vs_f16"] = rows["f16"]["ms"] / r["ms"]
-        if "f16+" in rows:
-            r["vs_f16p"] = rows["f16+"]["ms"] / r["ms"]
 
-    head = rows[args.headline]
+    head = formats[args.headline]
     # The step is one launch of the fused kernel (split-L pass + last-group LSE
     # merge), so its mean back-to-back duration over the timed region is the
     # kernel's launch duration; the split pass alone is reported beside it.
     step_gbs = head["gbps"]
     roofline = {"bound": "hbm", "achieved": step_gbs, "peak": PEAK_HBM_GBPS, "unit": "GB/s",
-                "frac": step_gbs / PEAK_HBM_GBPS, "traffic": load_traffic(f"{args.headline}_L{L}_G{G}"),
+                "frac": step_gbs / PEAK_HBM_GBPS, "traffic": load_traffic(f"{args.headline}_L{args.L}_G{G}"),
                 "kernel": f"decode_tiled<{args.headline}> fused (split-L pass + LSE merge, one launch per step)",
                 "algorithmic_bytes_per_launch": head["bytes"],
                 "kernel_ms": head["ms"], "frac_of_probed": step_gbs / ceiling,
-                "split_pass_only_ms": head["kernel_ms"], "split_pass_only_gbps": head["kernel_gbps"]}
-    cpu = None
+                "split_pass_only_ms": head["split_pass_ms"],
+                "split_pass_only_gbps": head["bytes"] / (head["split_pass_ms"] * 1e6)}
+    cpu = cpu0 = None
     if not args.no_cpu:
-        cpu = cpu_baseline(H, L, D, G)
-        log(f"cpu baseline: {cpu['value']:.3f} tok/s single-thread ({cpu['ms']:.0f} ms), "
-            f"{cpu['multithread']['value']:.2f} tok/s on {cpu['multithread']['cores']} threads")
+        cpu = cpu_baseline(H, args.L, D, G)
+        log(f"cpu baseline ({cpu['cpu_model']}, nproc {cpu['nproc']}): L={args.L}: {cpu['value']:.2f} tok/s "
+            f"on 1 core ({cpu['ms']:.1f} ms), {cpu['multithread']['value']:.1f} tok/s on "
+            f"{cpu['multithread']['cores']} threads ({cpu['multithread']['ms']:.2f} ms)")
+        cpu0 = cpu_reference(H, 4096, D, G, seconds=3.0)
+        g0 = {r["fmt"]: r for r in rows if r["L"] == 4096}
+        cpu0["gpu_rows"] = {f: {"ms": g0[f]["ms"], "tok_s": g0[f]["tok_s"]} for f in ("q8", "q8+") if f in g0}
+        log(f"configs[0] CPU path (q8 L=4096): {cpu0['ms']:.2f} ms = {cpu0['tok_s']:.1f} tok/s on 1 core, "
+            f"{cpu0['multithread']['ms']:.2f} ms = {cpu0['multithread']['tok_s']:.1f} tok/s on "
+            f"{cpu0['multithread']['cores']} threads; GPU " +
+            ", ".join(f"{f} {v['ms'] * 1e3:.1f} us = {v['tok_s']:.0f} tok/s" for f, v in cpu0["gpu_rows"].items()))
 
+    checked = None if args.no_check else all(r["checked"] for r in rows)
     line = {
         "metric": METRIC, "value": head["tok_s"], "unit": "tok/s", "n_gpus": 1,
         "steps": args.steps, "warmup": args.warmup, "ms_per_step": head["ms"],
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
         "dtype": "fp32", "data": "synthetic",
-        "config": {"workload": f"{args.headline} decode step, batch 1, H={H} D={D} L={L} G={G} "
-                               f"(BASELINE configs[1]-[3] shape)",
-                   "H": H, "D": D, "L": L, "G": G, "S": head["S"], "copies": head["copies"],
+        "config": {"workload": f"{args.headline} decode step, batch 1, H={H} D={D} L={args.L} G={G} "
+                               f"(BASELINE configs[2] shape; the metric's H32 D128 L16K)",
+                   "H": H, "D": D, "L": args.L, "G": G, "S": head["S"], "copies": head["copies"],
                    "storage": {"f16": "fp16", "f16+": "fp16", "q8": "int8", "q8+": "int8",
                                "q4": "int4", "q4+": "int4", "q3+": "int3"}[args.headline],
                    "parallelism": "single GPU, split-L"},
+        "checked": checked,
         "roofline": roofline,
         "cpu_baseline": cpu,
+        "cpu_configs0": cpu0,
         "probed_ceiling_gbps": ceiling,
         "mbu": head["mbu"],
-        "formats": rows,
+        "formats": formats,
+        "configs": rows,
         "extra": extra,
         "device": info["name"], "compute_units": info["compute_units"],
     }
     print(json.dumps(line), flush=True)
+    if checked is False:
+        log("bench.py: an output check FAILED: " +
+            ", ".join(f"{r['fmt']} L={r['L']}" for r in rows if not r["checked"]))
+        return 1
     return 0
 
 

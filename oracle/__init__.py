@@ -1,7 +1,7 @@
 """ctypes binding of the CPU oracle (oracle/liboracle.so).
 
 TEST INFRASTRUCTURE ONLY: imported by tests/, __graft_entry__.smoke() and
-bench.py's cpu_baseline leg, as the checker. The product (voltattn_amd) never
+bench.py's cpu_baseline leg and its after-timing output check, as the checker. The product (voltattn_amd) never
 imports it. See oracle.hpp for what each function restates and how it is pinned.
 """
 from __future__ import annotations
