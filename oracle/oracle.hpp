@@ -2,7 +2,8 @@
 //
 // TEST INFRASTRUCTURE ONLY. This library is the checker for the HIP product in
 // voltattn_amd/: only tests/, __graft_entry__.smoke() and bench.py's
-// cpu_baseline leg may link, load or call it. Nothing in the product path uses
+// cpu_baseline leg and after-timing output check may link, load or call it,
+// as the checker. Nothing in the product path uses
 // it, and the product must never fall back to it.
 //
 // What it restates (citations are src/voltattn.cu:line in the reference):
