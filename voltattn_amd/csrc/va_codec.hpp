@@ -9,8 +9,9 @@
 // per-element convert), once per row; `dot` and `axpy` then consume the pairs
 // for every query head that shares the row (grouped-query attention reuses
 // one unpack for several heads):
-//   * K: v_dot2_f32_f16 against the unscaled fp16 q (f16, q8, q4: products of
-//     two fp16 values are exact in fp32), or v_fma_mix_f32 against fp32 q (q3);
+//   * K: v_dot2_f32_f16 against the fp16 q slice (products of two fp16 values
+//     are exact in fp32): unscaled for f16, q8 and q4, pre-scaled per element
+//     by a power of two for q3;
 //   * V: v_fma_mix_f32, o_e += ev * code_e with an fp16 operand and fp32
 //     accumulation (P.V stays fp32).
 // The fp16 "magic" construction: OR-ing a code n (< 2^10 / 2^r) shifted left by
@@ -209,8 +210,12 @@ template <> struct Codec<KQ4> {
 // and one at bit 16 + r' of the high half, r, r' <= 7. The 16 pairs:
 //   window s = 0, 6, 12, 36, 42, 48: (a, a+6) at (0, 18) and (a+1, a+7) at (3, 21), a = s/3
 //   window s = 68, 74:               (a, a+4) at (4, 16) and (a+1, a+5) at (7, 19), a = (s+4)/3
-// A pair becomes (2^r v, 2^r' v') exactly; K uses fp32 q pre-scaled by 2^-r,
-// V accumulates 2^r v and finish() scales o_e by 2^-r once.
+// A pair becomes (2^r v, 2^r' v') exactly. K goes through v_dot2_f32_f16
+// against an fp16 q pair pre-scaled per element by 2^(k - r): each product
+// 2^r v * q 2^(k - r) = q v 2^k is exact in fp32, and the lane's power of two
+// k (max |q| * 2^k in [2^14, 2^15)) keeps every scaled q that matters normal;
+// 2^-k is folded into the final scale. V accumulates 2^r v and finish() scales
+// o_e by 2^-r once.
 struct Q3Pair { int a, b, s, r, rp; };
 __device__ constexpr Q3Pair kQ3Pairs[16] = {
     {0, 6, 0, 0, 2},    {1, 7, 0, 3, 5},    {2, 8, 6, 0, 2},    {3, 9, 6, 3, 5},
@@ -228,7 +233,7 @@ __device__ constexpr int q3_shift(int e) {          // r of element e in its pai
 
 template <> struct Codec<KQ3> {
     static constexpr int EPL = 32, NP = 16;
-    struct QReg { float q[32]; };
+    struct QReg { h2 q[NP]; float qs; };     // q[i] = (q_a 2^(k - r), q_b 2^(k - r')) of pair i
     __device__ static uint32_t window(const u32x3& w, int s) {
         if (s == 0) return w.x;
         if (s < 32) return __builtin_amdgcn_alignbit(w.y, w.x, s);
@@ -246,11 +251,20 @@ template <> struct Codec<KQ3> {
     __device__ static void load_q(QReg& r, const uint16_t* qh, float qs) {
         uint32_t qw[16];
         load_q_words<32>(qw, qh);
+        float x[32], mx = 0.f;
 #pragma unroll
         for (int e = 0; e < 32; ++e) {
-            const float x = (e & 1) ? h2f_hi(qw[e / 2]) : h2f_lo(qw[e / 2]);
-            r.q[e] = x * qs * (1.0f / (float)(1 << q3_shift(e)));
+            x[e] = (e & 1) ? h2f_hi(qw[e / 2]) : h2f_lo(qw[e / 2]);
+            mx = fmaxf(mx, __builtin_fabsf(x[e]));
         }
+        // k: max |q| * 2^k in [2^14, 2^15) (frexp exponent e: mx = m 2^e, m in [0.5, 1));
+        // an all-zero slice keeps k = 0
+        const int k = mx > 0.f ? 15 - __builtin_amdgcn_frexp_expf(mx) : 0;
+#pragma unroll
+        for (int i = 0; i < NP; ++i)
+            r.q[i] = hh(__builtin_ldexpf(x[kQ3Pairs[i].a], k - kQ3Pairs[i].r),
+                        __builtin_ldexpf(x[kQ3Pairs[i].b], k - kQ3Pairs[i].rp));
+        r.qs = __builtin_ldexpf(qs, -k);
     }
     __device__ static uint32_t magic() { uint32_t m; VA_VGPR_CONST(m, 0x64006400); return m; }
     template <int... I>
@@ -264,12 +278,11 @@ template <> struct Codec<KQ3> {
     __device__ static float dot(const h2 (&p)[NP], const QReg& r) {
         float a0 = 0.f, a1 = 0.f;
 #pragma unroll
-        for (int i = 0; i < NP; ++i) {
-            float& a = (i & 1) ? a1 : a0;
-            a = __builtin_fmaf((float)p[i].x, r.q[kQ3Pairs[i].a], a);
-            a = __builtin_fmaf((float)p[i].y, r.q[kQ3Pairs[i].b], a);
+        for (int i = 0; i < NP; i += 2) {
+            a0 = __builtin_amdgcn_fdot2(p[i], r.q[i], a0, false);
+            a1 = __builtin_amdgcn_fdot2(p[i + 1], r.q[i + 1], a1, false);
         }
-        return a0 + a1;
+        return (a0 + a1) * r.qs;
     }
     __device__ static void axpy(const h2 (&p)[NP], float ev, float* o) {
 #pragma unroll
