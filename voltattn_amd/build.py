@@ -47,6 +47,10 @@ HIPCC_FLAGS = [
     # MFMA accumulators in arch VGPRs (the matrix-core decode fits in 256 of
     # them); the AGPR form shuttled them through v_accvgpr moves.
     "-mllvm", "-amdgpu-mfma-vgpr-form=1",
+    # Kernel argument preload: the first 16 dwords of scalar kernel arguments
+    # arrive in SGPRs with the wave (the code object keeps a prologue that
+    # loads them itself where the firmware does not preload).
+    "-mllvm", "-amdgpu-kernarg-preload-count=16",
 ]
 
 

@@ -188,7 +188,8 @@ static hipError_t launch_one(bool tiled, int H, const DecodeArgs& a, hipStream_t
     const dim3 grid((unsigned)(H * a.S));
     if (tiled) {
         using T = TiledShape<KIND>;
-        hipLaunchKernelGGL((decode_tiled<KIND, D, G, T::U, T::waves, 1, false>), grid, dim3(T::waves * 64), 0, st, a);
+        hipLaunchKernelGGL((decode_tiled<KIND, D, G, T::U, T::waves, 1, false>), grid, dim3(T::waves * 64), 0, st,
+                           VA_TILED_ARGS(a));
     } else {
         if constexpr (KIND == KQ3) return hipErrorInvalidValue;
         else hipLaunchKernelGGL((decode_w1<KIND, D, G>), grid, dim3(256), 0, st, a);

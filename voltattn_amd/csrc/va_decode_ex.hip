@@ -139,7 +139,7 @@ static hipError_t launch_ex(int groups, const DecodeArgs& a, hipStream_t st) {
         constexpr int U = ex_unroll<KIND, D, QG>();
         static_assert(Tile<KIND, D>::PPW * U <= 64, "a wave tile must fit the smallest page");
         hipLaunchKernelGGL((decode_tiled<KIND, D, G, U, Cfg::WAVES, QG, PAGED, Cfg::MINB>),
-                           dim3((unsigned)(groups * a.S)), dim3(Cfg::WAVES * 64), 0, st, a);
+                           dim3((unsigned)(groups * a.S)), dim3(Cfg::WAVES * 64), 0, st, VA_TILED_ARGS(a));
         return hipGetLastError();
     }
 }

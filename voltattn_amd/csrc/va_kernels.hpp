@@ -34,6 +34,11 @@ struct DecodeArgs {
     int   num_pages;        // pages in the pool (ids outside [0, num_pages) are rejected)
 };
 
+// Launch of the tiled decode kernel: the leading scalar arguments (preloaded
+// into SGPRs) followed by the rest of the DecodeArgs.
+#define VA_TILED_ARGS(a) (a).k, (a).v, (a).sk, (a).sv, (a).L, (a).S, (a).chunk, (a).ticket_slot, (a).q, \
+    ((a).ticket_slot >= 0 ? static_cast<void*>((a).out) : static_cast<void*>((a).ws)), (a)
+
 // Fused second pass: per-(slot, merge group) ticket lines in static device
 // memory (zero at load): word 0 counts the arrivals of the group's
 // work-groups, word 1 is the group's call epoch (tagged protocol), advanced by

@@ -47,8 +47,29 @@ namespace va {
 constexpr float RESCALE_SLACK = 8.0f;    // log2 units: weights stay <= 256
 constexpr float M_INIT = -1e30f;         // finite "no score yet" maximum
 
+// log2(e) / sqrt(D), as the host computes it (double, then rounded to float).
+template <int D>
+__device__ constexpr float qscale_of() {
+    static_assert(D == 64 || D == 128, "head dimension");
+    return (float)(1.4426950408889634074 / (D == 128 ? 11.313708498984760390 : 8.0));
+}
+
+// What the first tile needs comes first as plain scalars (14 dwords: k, v,
+// sk, sv, L, S, chunk, slot, q), so the hardware preloads them into SGPRs
+// before the wave starts (kernel argument preload) and the first loads issue
+// without waiting for a kernarg fetch; dst (`out` for the fused merge, slot
+// >= 0; `ws` for the two-pass form) and `rest` (grouped-query and paged
+// fields) are read from the kernarg segment when needed.
 template <int KIND, int D, int G, int U, int WAVES, int QG, bool PAGED, int MINB = 1>
-__global__ __launch_bounds__(WAVES * 64, MINB) void decode_tiled(DecodeArgs a) {
+__global__ __launch_bounds__(WAVES * 64, MINB) void decode_tiled(
+    const uint8_t* k, const uint8_t* v, const uint16_t* sk, const uint16_t* sv,
+    int L_, int S_, int chunk_, int slot_, const uint16_t* q, void* dst, DecodeArgs rest) {
+    DecodeArgs a = rest;
+    a.k = k; a.v = v; a.sk = sk; a.sv = sv; a.q = q;
+    a.out = static_cast<uint16_t*>(dst);
+    a.ws = static_cast<float*>(dst);
+    a.L = L_; a.S = S_; a.chunk = chunk_; a.ticket_slot = slot_;
+    a.qscale = qscale_of<D>();
     using T = Tile<KIND, D>;
     using C = Codec<KIND>;
     using LoadT = typename LaneLoad<KIND>::type;
