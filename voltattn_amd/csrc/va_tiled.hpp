@@ -300,8 +300,15 @@ __global__ __launch_bounds__(WAVES * 64, MINB) void decode_tiled(
         // (An exit inside the loop instead measured 1.5 us slower for the paged
         // one-slot form: it changes how the loop body is scheduled.)
         const int npair = niter / 2;
+        // f16 rows in 8-wave groups: the older wave of each SIMD pair wins issue
+        // and runs ahead, and the younger one finishes alone with half the loads
+        // in flight. On long splits a barrier per tile pair keeps the waves
+        // together (measured on MI355X, H=32 D=128: L=65536 165.7 -> 161.3 us);
+        // below 16 tiles per group it costs more than it saves (L=4096 +0.35 us).
+        const bool lockstep = KIND == KF16 && WAVES == 8 && QG == 1 && !PAGED && niter >= 16;
         for (int ip = 0; ip < npair; ++ip) {
             const int it = 2 * ip;
+            if (lockstep) __builtin_amdgcn_s_barrier();     // niter is uniform over the group
             stage_scales(ska, sva);
             load_tile(it + 1, kb, vb, skb, svb);
             compute_tile(it, ka, va_);
