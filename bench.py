@@ -134,7 +134,7 @@ class Workload:
         self.bufs = []
 
 
-def time_workload(va, w: Workload, steps: int, warmup: int, stream) -> dict:
+def time_workload(va, w: Workload, steps: int, warmup: int, stream, steps_only: bool = False) -> dict:
     H, L, D, G, S, fmt = w.H, w.L, w.D, w.G, w.S, w.fmt
     bufs = [w.bufs_for(c) for c in range(w.copies)]
     launch = lambda c: va.launch(fmt, bufs[c % w.copies], H, L, D, S, G=G, stream=stream)
@@ -163,6 +163,8 @@ def time_workload(va, w: Workload, steps: int, warmup: int, stream) -> dict:
         e1.synchronize()
         va.sync()
         mean_ms = e0.elapsed_ms(e1) / steps
+        if steps_only:            # profiling runs: only fused steps of this shape are dispatched
+            return {"mean_ms": mean_ms, "best_ms": float("nan"), "kernel_ms": float("nan")}
         # (2) reference method: best single launch, each behind an untimed lead launch
         best_ms = float("inf")
         for i in range(steps):
@@ -427,6 +429,9 @@ def main() -> int:
     ap.add_argument("--set-gib", type=float, default=2.0, help="rotated working set per row")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-check", action="store_true", help="skip the after-timing output check")
+    ap.add_argument("--steps-only", action="store_true",
+                    help="time only the back-to-back steps (no best-single or split-pass launches), so a "
+                         "profiler's per-kernel statistics cover fused steps of one shape")
     ap.add_argument("--no-extra", action="store_true",
                     help="skip the grouped-query and paged workloads (reported under 'extra')")
     ap.add_argument("--copy-probe-mib", type=int, default=0,
@@ -477,7 +482,7 @@ def main() -> int:
         try:
             S = args.splits or va.pick_splits(fmt, H, L, D)
             w.set_splits(S)
-            t = time_workload(va, w, args.steps, args.warmup, stream)
+            t = time_workload(va, w, args.steps, args.warmup, stream, args.steps_only)
             chk = {"checked": None} if args.no_check else check_workload(va, w, (0, H // 2, H - 1))
         finally:
             w.free()
@@ -539,7 +544,7 @@ def main() -> int:
                 "algorithmic_bytes_per_launch": head["bytes"],
                 "kernel_ms": head["ms"], "frac_of_probed": step_gbs / ceiling,
                 "split_pass_only_ms": head["split_pass_ms"],
-                "split_pass_only_gbps": head["bytes"] / (head["split_pass_ms"] * 1e6)}
+                "split_pass_only_gbps": head["bytes"] / (head["split_pass_ms"] * 1e6) if head["split_pass_ms"] > 0 else None}
     cpu = cpu0 = None
     if not args.no_cpu:
         cpu = cpu_baseline(H, args.L, D, G)
