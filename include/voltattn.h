@@ -51,8 +51,16 @@ enum {
 
 /* Formats: the reference's enum class Fmt {F16, F16M, Q8, Q8M, Q4, Q4M, Q3M}
  * (src/voltattn.cu:676). The "+" formats select the tiled multi-position
- * kernels; the others the naive one-position-per-wave kernels. */
-typedef enum {
+ * kernels; the others the naive one-position-per-wave kernels. The type is an
+ * int in C and C++ alike: under C++ it is given that underlying type, so a
+ * caller's out-of-range value is still a valid va_fmt that the entry points
+ * reject with VA_EINVAL (rather than undefined behaviour). */
+#ifdef __cplusplus
+#define VA_ENUM_BASE : int
+#else
+#define VA_ENUM_BASE
+#endif
+typedef enum VA_ENUM_BASE {
     VA_F16  = 0,   /* f16   naive  (attn_f16,     src/voltattn.cu:122-187) */
     VA_F16P = 1,   /* f16+  tiled  (attn_f16_mlp, src/voltattn.cu:364-423) */
     VA_Q8   = 2,   /* q8    naive  (attn_q8,      src/voltattn.cu:189-252) */

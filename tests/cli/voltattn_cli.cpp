@@ -6,6 +6,11 @@
 //                           C++ mirror (voltattn.hpp), 42 cases
 //   voltattn --probe        HBM read ceiling
 //   voltattn --bench        selftest gate, probe, then the format x L table
+//   voltattn --selftest-host  the selftest's host side alone, no GPU: every
+//                           case's inputs (draws, quantizer, dequantizer) and
+//                           double reference, and the split-L merge algebra of
+//                           each case's S against it (the sanitizer build runs
+//                           this)
 //
 // Bench options: --G 32|64 (default 32), --L 4096,16384,65536, --fmt f16,q8+,...,
 // --reps N (default 20), --set-gib X (rotated working set, default 2),
@@ -93,6 +98,43 @@ int selftest() {
     }
     if (fails) { std::printf("%d of %d case(s) FAILED\n", fails, n); return 1; }
     std::printf("all %d cases passed\n", n);
+    return 0;
+}
+
+// The selftest's host side on its own (no device): the inputs and double
+// reference of every case, the packed payload and scale sizes of each format,
+// and the S-split log-sum-exp algebra (chunk = ceil(L/S), src/voltattn.cu:804,
+// merge src/voltattn.cu:651-672) against the unsplit reference.
+int selftest_host() {
+    int n = 0, fails = 0;
+    for (int G : {64, 32}) {
+        for (Fmt f : kAllFormats) {
+            if (is_f16(f) && G != 64) continue;
+            for (const Case& c : kCases) {
+                const uint32_t seed = oracle::selftest_seed(c.H, c.L, c.D, c.S);
+                const oracle::CaseData cd = oracle::make_case(qbits(f), c.H, c.L, c.D, G, seed);
+                const size_t nel = (size_t)c.H * c.L * c.D;
+                bool ok = cd.kd.size() == nel && cd.vd.size() == nel && cd.ref.size() == (size_t)c.H * c.D &&
+                          cd.kpay.size() == va_payload_bytes((va_fmt)f, c.H, c.L, c.D);
+                if (!is_f16(f)) ok = ok && cd.kscale.size() * 2 == va_scale_bytes((va_fmt)f, c.H, c.L, c.D, G);
+                const std::vector<float> split = oracle::split_attention(cd.kd.data(), cd.vd.data(), cd.q.data(),
+                                                                         c.H, c.L, c.D, c.S, nullptr, nullptr);
+                double maxdiff = 0.0;
+                for (size_t i = 0; i < split.size(); ++i)
+                    maxdiff = std::max(maxdiff, std::fabs((double)split[i] - (double)cd.ref[i]));
+                ok = ok && maxdiff <= 1e-6;
+                std::printf("%-4s  H=%-3d L=%-5d D=%-3d S=%-2d G=%-2d  split-vs-reference %.1e  %s\n", fmt_name(f),
+                            c.H, c.L, c.D, c.S, G, maxdiff, ok ? "ok" : "FAIL");
+                fails += !ok;
+                ++n;
+            }
+        }
+    }
+    if (fails) {
+        std::printf("host selftest: %d of %d case(s) FAILED\n", fails, n);
+        return 1;
+    }
+    std::printf("host selftest: all %d cases ok\n", n);
     return 0;
 }
 
@@ -561,7 +603,9 @@ int main(int argc, char** argv) {
                 if (i + 1 >= argc) throw std::runtime_error("missing value for " + a);
                 return argv[++i];
             };
-            if (a == "--selftest" || a == "--selftest-ex" || a == "--bench" || a == "--probe") mode = a;
+            if (a == "--selftest" || a == "--selftest-ex" || a == "--selftest-host" || a == "--bench" ||
+                a == "--probe")
+                mode = a;
             else if (a == "--G") G = std::stoi(next());
             else if (a == "--reps") reps = std::max(1, std::stoi(next()));
             else if (a == "--set-gib") set_gib = std::stod(next());
@@ -576,6 +620,7 @@ int main(int argc, char** argv) {
             return 0;
         }
         if (mode == "--selftest-ex") return selftest_ex();
+        if (mode == "--selftest-host") return selftest_host();
         const int rc = selftest();                             // --bench is gated on it (src/voltattn.cu:1075)
         if (rc || mode == "--selftest") return rc;
         std::printf("\n");

@@ -10,6 +10,10 @@
   grouped-query q8/q4 kernels in their vector-ALU form (``VA_GQA_MFMA=0``):
   the comparison build ``tests/test_gpu_valu_form.py`` runs. Only
   ``va_decode_ex.hip`` differs; the other objects are the product's.
+* ``build/variants/libvoltattn_hip_hostsan.so`` — the C ABI unit
+  (``va_runtime.hip``) with its host code built under AddressSanitizer and
+  UndefinedBehaviorSanitizer (device code unchanged), for the CPU sanitizer
+  run of ``tests/test_sanitizers.py``.
 * ``oracle/liboracle.so`` — the CPU checker (test infrastructure, g++).
 * ``build/voltattn`` — the C++ selftest/bench/probe harness (tests/cli), linked
   against both.
@@ -68,9 +72,14 @@ def _run(cmd: list[str], cwd: Path | None = None) -> None:
 
 
 VARIANTS = {
-    # name: (translation unit rebuilt with the defines, defines)
-    "valu": ("va_decode_ex.hip", ("VA_GQA_MFMA=0",)),
+    # name: (translation unit rebuilt, its defines, its extra compiler flags)
+    "valu": ("va_decode_ex.hip", ("VA_GQA_MFMA=0",), ()),
+    # host code only: each -fsanitize= goes to the host compilation
+    "hostsan": ("va_runtime.hip", (), ("-Xarch_host", "-fsanitize=address", "-Xarch_host", "-fsanitize=undefined",
+                                       "-Xarch_host", "-fno-sanitize-recover=all", "-Xarch_host", "-fno-omit-frame-pointer",
+                                       "-Xarch_host", "-g")),
 }
+VARIANT_LINK = {"hostsan": ("-fsanitize=address", "-fsanitize=undefined")}
 VARIANT_DIR = ROOT / "build" / "variants"
 
 
@@ -78,11 +87,11 @@ def variant_path(name: str) -> Path:
     return VARIANT_DIR / f"libvoltattn_hip_{name}.so"
 
 
-def _link(cc: str, objs, out: Path) -> Path:
+def _link(cc: str, objs, out: Path, flags=()) -> Path:
     out = Path(out)
     out.parent.mkdir(parents=True, exist_ok=True)
     tmp = out.with_suffix(".so.tmp")
-    _run([cc, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *map(str, objs)])
+    _run([cc, f"--offload-arch={ARCH}", "-shared", "-fPIC", *flags, "-o", str(tmp), *map(str, objs)])
     os.replace(tmp, out)
     return out
 
@@ -99,10 +108,11 @@ def build_library(jobs: int = 8, out: Path = LIB, defines: tuple[str, ...] = (),
     dflags = [f"-D{d}" for d in defines]
     jobs_list = [(src, obj_dir / (src.stem + ".o"), dflags) for src in srcs]
     for name in variants:
-        unit, vdefs = VARIANTS[name]
+        unit, vdefs, vflags = VARIANTS[name]
         vdir = obj_dir / f"variant_{name}"
         vdir.mkdir(parents=True, exist_ok=True)
-        jobs_list.append((CSRC / unit, vdir / (Path(unit).stem + ".o"), dflags + [f"-D{d}" for d in vdefs]))
+        jobs_list.append((CSRC / unit, vdir / (Path(unit).stem + ".o"),
+                          dflags + [f"-D{d}" for d in vdefs] + list(vflags)))
 
     def compile_one(job) -> Path:
         src, obj, fl = job
@@ -116,7 +126,7 @@ def build_library(jobs: int = 8, out: Path = LIB, defines: tuple[str, ...] = (),
     for i, name in enumerate(variants):
         unit = VARIANTS[name][0]
         vobjs = [o for o in main_objs if o.stem != Path(unit).stem] + [objs[len(srcs) + i]]
-        _link(cc, vobjs, variant_path(name))
+        _link(cc, vobjs, variant_path(name), VARIANT_LINK.get(name, ()))
     return Path(out)
 
 
