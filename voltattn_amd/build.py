@@ -72,8 +72,12 @@ def _run(cmd: list[str], cwd: Path | None = None) -> None:
 
 
 VARIANTS = {
-    # name: (translation unit rebuilt, its defines, its extra compiler flags)
+    # name: (translation unit(s) rebuilt, their defines, their extra compiler flags)
     "valu": ("va_decode_ex.hip", ("VA_GQA_MFMA=0",), ()),
+    # test only: every fused merge gives up after its bounded wait (NaN output,
+    # counted for va_merge_faults), so the failure path runs with kernels that
+    # all exit normally
+    "lost": (("va_decode.hip", "va_decode_ex.hip"), ("VA_TEST_LOSE_MERGES=1",), ()),
     # host code only: each -fsanitize= goes to the host compilation
     "hostsan": ("va_runtime.hip", (), ("-Xarch_host", "-fsanitize=address", "-Xarch_host", "-fsanitize=undefined",
                                        "-Xarch_host", "-fno-sanitize-recover=all", "-Xarch_host", "-fno-omit-frame-pointer",
@@ -107,12 +111,17 @@ def build_library(jobs: int = 8, out: Path = LIB, defines: tuple[str, ...] = (),
     cc = hipcc()
     dflags = [f"-D{d}" for d in defines]
     jobs_list = [(src, obj_dir / (src.stem + ".o"), dflags) for src in srcs]
+    vjobs = {}
     for name in variants:
-        unit, vdefs, vflags = VARIANTS[name]
+        units, vdefs, vflags = VARIANTS[name]
+        units = (units,) if isinstance(units, str) else units
         vdir = obj_dir / f"variant_{name}"
         vdir.mkdir(parents=True, exist_ok=True)
-        jobs_list.append((CSRC / unit, vdir / (Path(unit).stem + ".o"),
-                          dflags + [f"-D{d}" for d in vdefs] + list(vflags)))
+        vjobs[name] = []
+        for unit in units:
+            vjobs[name].append(len(jobs_list))
+            jobs_list.append((CSRC / unit, vdir / (Path(unit).stem + ".o"),
+                              dflags + [f"-D{d}" for d in vdefs] + list(vflags)))
 
     def compile_one(job) -> Path:
         src, obj, fl = job
@@ -123,9 +132,10 @@ def build_library(jobs: int = 8, out: Path = LIB, defines: tuple[str, ...] = (),
         objs = list(ex.map(compile_one, jobs_list))
     main_objs = objs[:len(srcs)]
     _link(cc, main_objs, out)
-    for i, name in enumerate(variants):
-        unit = VARIANTS[name][0]
-        vobjs = [o for o in main_objs if o.stem != Path(unit).stem] + [objs[len(srcs) + i]]
+    for name in variants:
+        rebuilt = [objs[i] for i in vjobs[name]]
+        stems = {o.stem for o in rebuilt}
+        vobjs = [o for o in main_objs if o.stem not in stems] + rebuilt
         _link(cc, vobjs, variant_path(name), VARIANT_LINK.get(name, ()))
     return Path(out)
 

@@ -22,6 +22,14 @@ static __device__ __align__(256) float g_partf[(size_t)TICKET_SLOTS * PART_CAP *
 
 constexpr int POLL_MAX = 1 << 12;   // bound on re-reads of one in-flight word
 
+// Test builds only (a comparison library, never the product): every fused
+// merge waits for something that never comes, a tag no partial carries or one
+// more count than there are groups, so it gives up after its bounded wait,
+// stores NaN and counts the loss; every kernel still exits normally.
+#ifndef VA_TEST_LOSE_MERGES
+#define VA_TEST_LOSE_MERGES 0
+#endif
+
 // Merges of this code object that gave up waiting for a partial (NaN output);
 // read by the host through read_lost_merges().
 static __device__ unsigned g_lost_merges;
@@ -131,6 +139,7 @@ __device__ void finish_tagged(const DecodeArgs& a, const Route& rt, const float 
         s_last = __hip_atomic_fetch_add(ticket, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
                  (unsigned)(S - 1);
     const uint32_t tag = (epoch << 11) | ((uint32_t)rt.mg << 1) | 1u;
+    const uint32_t want = VA_TEST_LOSE_MERGES ? tag ^ 0x80000000u : tag;   // the merger's expected tag
     uint64_t* base = g_parts + ((size_t)a.ticket_slot * PART_CAP + (size_t)rt.mg * QG * S) * PART_STRIDE;
     if (t < D) {
 #pragma unroll
@@ -184,7 +193,7 @@ __device__ void finish_tagged(const DecodeArgs& a, const Route& rt, const float 
         // Selection is branch-free and the rare re-read loop is wave-uniform (all
         // lanes run it, stale lanes take the new value).
         for (int k = 0; k < POLL_MAX; ++k) {     // rare: stores still in flight
-            const bool need = in_s && !own && !(mt == tag && lt == tag);
+            const bool need = in_s && !own && !(mt == want && lt == want);
             if (__builtin_amdgcn_ballot_w64(need) == 0) break;
             __builtin_amdgcn_s_sleep(2);
             const u32x4 re = ld128_dev(rp, (uint32_t)jl * PB);
@@ -194,7 +203,7 @@ __device__ void finish_tagged(const DecodeArgs& a, const Route& rt, const float 
             lv = need ? rlv : lv;
             lt = need ? rlt : lt;
         }
-        good = good && (!in_s || own || (mt == tag && lt == tag));
+        good = good && (!in_s || own || (mt == want && lt == want));
         const float own_m = s_own[qw][D], own_l = s_own[qw][D + 1];
         const float mj = !in_s ? -__builtin_inff() : own ? own_m : __builtin_bit_cast(float, mv);
         const float lj = !in_s ? 0.f : own ? own_l : __builtin_bit_cast(float, lv);
@@ -215,7 +224,7 @@ __device__ void finish_tagged(const DecodeArgs& a, const Route& rt, const float 
                 } else {
                     uint32_t a0 = op[i][0], t0 = op[i][1], a1 = op[i][2], t1 = op[i][3];
                     for (int k = 0; k < POLL_MAX; ++k) {
-                        const bool need = !(t0 == tag && t1 == tag);
+                        const bool need = !(t0 == want && t1 == want);
                         if (__builtin_amdgcn_ballot_w64(need) == 0) break;
                         __builtin_amdgcn_s_sleep(2);
                         const u32x4 re = ld128_dev(rp, (uint32_t)j * PB + 16u + (uint32_t)dp * 16u);
@@ -225,7 +234,7 @@ __device__ void finish_tagged(const DecodeArgs& a, const Route& rt, const float 
                         a1 = need ? ra1 : a1;
                         t1 = need ? rt1 : t1;
                     }
-                    good = good && t0 == tag && t1 == tag;
+                    good = good && t0 == want && t1 == want;
                     v0 = __builtin_bit_cast(float, a0);
                     v1 = __builtin_bit_cast(float, a1);
                 }
@@ -337,12 +346,13 @@ __device__ void finish_counted(const DecodeArgs& a, const Route& rt, const float
         }
     }
     if (t == 0) {                                // the other S - 1 partials stored?
+        const unsigned need = (unsigned)(S - 1 + VA_TEST_LOSE_MERGES);
         unsigned n = load_dev(line + 2);
-        for (int k = 0; k < POLL_MAX && n < (unsigned)(S - 1); ++k) {
+        for (int k = 0; k < POLL_MAX && n < need; ++k) {
             __builtin_amdgcn_s_sleep(2);
             n = load_dev(line + 2);
         }
-        s_bad = n < (unsigned)(S - 1);
+        s_bad = n < need;
         if (s_bad) count_lost_merge();
     }
     __syncthreads();                             // the partial loads below are served from the coherence point (sc1)
