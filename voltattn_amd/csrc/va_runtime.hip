@@ -10,6 +10,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <atomic>
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
@@ -135,15 +136,17 @@ int run_splits(va_fmt fmt, const va_bufs* b, int H, int L, int D, int G, int S, 
     return VA_OK;
 }
 
-int g_cu_count = 0;
+std::atomic<int> g_cu_count{0};
 
+// CUs of the first device asked (the split rule assumes identical devices).
 int cu_count() {
-    if (g_cu_count > 0) return g_cu_count;
+    const int c = g_cu_count.load(std::memory_order_relaxed);
+    if (c > 0) return c;
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess) return 0;
     int n = 0;
     if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
-    g_cu_count = n;
+    g_cu_count.store(n, std::memory_order_relaxed);
     return n;
 }
 
@@ -766,18 +769,23 @@ int va_graph_end(void* stream, void** graph_exec) {
     hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
     unsigned long long id = 0;
     VA_HIP(hipStreamGetCaptureInfo(as_stream(stream), &cs, &id), "hipStreamGetCaptureInfo");
+    const unsigned long long capture = cs == hipStreamCaptureStatusActive ? (id | (1ull << 63)) : 0ull;
     hipGraph_t g = nullptr;
-    VA_HIP(hipStreamEndCapture(as_stream(stream), &g), "hipStreamEndCapture");
+    hipError_t e = hipStreamEndCapture(as_stream(stream), &g);
+    if (e != hipSuccess) {                       // no graph: nothing can replay the capture's slots
+        g_slots.release_capture(capture);
+        return hip_fail(e, "hipStreamEndCapture");
+    }
     hipGraphExec_t x = nullptr;
-    const hipError_t e = hipGraphInstantiate(&x, g, nullptr, nullptr, 0);
+    e = hipGraphInstantiate(&x, g, nullptr, nullptr, 0);
     (void)hipGraphDestroy(g);
     if (e != hipSuccess) {
-        if (cs == hipStreamCaptureStatusActive) g_slots.release_capture(id | (1ull << 63));
+        g_slots.release_capture(capture);
         return hip_fail(e, "hipGraphInstantiate");
     }
-    if (cs == hipStreamCaptureStatusActive) {
+    if (capture) {
         std::lock_guard<std::mutex> lock(g_graph_mu);
-        g_graph_capture[x] = id | (1ull << 63);
+        g_graph_capture[x] = capture;
     }
     *graph_exec = x;
     return VA_OK;
