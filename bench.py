@@ -34,6 +34,9 @@ Method (reference bench, src/voltattn.cu:967-1070, re-derived for MI355X):
     payload + fp16 scales: 2*H*L*(D*b/8 + 2*D/G)) over the fused decode
     kernel's mean launch time (the K back-to-back steps between events: one
     launch per step); the split pass alone (va_decode_splits) beside it;
+  * launch floor (va_probe_launch): us per back-to-back launch of an empty
+    kernel with the decode step's grid, the fixed cost every step pays
+    outside its own work (reported as launch_floor_us);
   * cpu_baseline: the oracle's double-precision reference attention
     (reference(), src/voltattn.cu:769-794) on the headline shape, timed on
     this host (rank 0, N=1 only); `cpu_configs0` is the same on configs[0]
@@ -453,6 +456,8 @@ def main() -> int:
         f"mem={info['total_mem'] / 2**30:.0f} GiB")
     ceiling = va.probe_read(int(args.probe_gib * 2**30), reps=5)
     log(f"probed read ceiling: {ceiling:.1f} GB/s ({args.probe_gib:g} GiB buffer)")
+    launch_floor = va.probe_launch(2000)
+    log(f"launch floor: {launch_floor:.2f} us per back-to-back launch of an empty kernel on the decode grid")
 
     if args.copy_probe_mib > 0:
         nb = args.copy_probe_mib << 20
@@ -576,6 +581,7 @@ def main() -> int:
         "cpu_baseline": cpu,
         "cpu_configs0": cpu0,
         "probed_ceiling_gbps": ceiling,
+        "launch_floor_us": launch_floor,
         "mbu": head["mbu"],
         "formats": formats,
         "configs": rows,

@@ -170,6 +170,13 @@ int va_fill_normal(float* x, size_t n, uint64_t seed, void* stream);
  * (probe_ceiling + read_kernel, src/voltattn.cu:64-78, 935-957). */
 int va_probe_read(size_t bytes, int reps, double* best_gbps);
 
+/* Launch floor: microseconds per launch of an empty kernel with one 256-thread
+ * work-group per CU (the decode step's grid at H*S = CUs), `launches` of them
+ * back to back on a private stream after a warm-up: the fixed cost each decode
+ * step pays outside its own work. No counterpart in the reference (its bench
+ * reports only the read ceiling); a measurement aid like va_probe_read. */
+int va_probe_launch(int launches, double* us_per_launch);
+
 /* ---- grouped-query attention, batches and paged caches ----
  * No counterpart in the reference, which decodes one sequence with one query
  * head per K/V head from a contiguous cache (its README.md:205-206 lists GQA

@@ -146,3 +146,12 @@ def test_pick_splits_rule():
         assert va.split_chunk(L, S) >= 4096 or S == 8
     assert va.pick_splits(va.Fmt.Q3M, 8, 65536, 128) == 32
     assert va.pick_splits(va.Fmt.Q3M, 8, 262144, 128) == 64
+
+
+def test_probe_argument_checks():
+    d = C.c_double(0.0)
+    assert va.lib.va_probe_launch(10, None) == VA_ENULL
+    assert va.lib.va_probe_launch(0, C.byref(d)) == VA_EINVAL
+    assert va.lib.va_probe_launch(2000000, C.byref(d)) == VA_EINVAL
+    assert va.lib.va_probe_read(1 << 30, 1, None) == VA_ENULL
+    assert va.lib.va_probe_read(1024, 1, C.byref(d)) == VA_EINVAL       # below 1 MiB

@@ -106,6 +106,7 @@ _sig("va_quantize", _I, _I, _I, _P, _SZ, _I, _P, _P, _P)
 _sig("va_f32_to_f16", _I, _P, _SZ, _P, _P)
 _sig("va_fill_normal", _I, _P, _SZ, _U64, _P)
 _sig("va_probe_read", _I, _SZ, _I, C.POINTER(C.c_double))
+_sig("va_probe_launch", _I, _I, C.POINTER(C.c_double))
 _sig("va_decode_gqa", _I, _I, C.POINTER(_Bufs), _I, _I, _I, _I, _I, _I, _P)
 _sig("va_pick_splits_gqa", _I, _I, _I, _I, _I, _I, C.POINTER(_I))
 _sig("va_decode_paged", _I, _I, C.POINTER(_PagedBufs), C.POINTER(_PagedShape), _I, _P)
@@ -352,6 +353,13 @@ def probe_read(nbytes: int, reps: int = 10) -> float:
     g = C.c_double(0.0)
     check(lib.va_probe_read(nbytes, reps, C.byref(g)))
     return g.value
+
+
+def probe_launch(launches: int = 2000) -> float:
+    """Microseconds per back-to-back launch of an empty kernel on the decode grid."""
+    us = C.c_double(0.0)
+    check(lib.va_probe_launch(launches, C.byref(us)))
+    return us.value
 
 
 def device_count() -> int:

@@ -105,6 +105,9 @@ hipError_t launch_merge(const float* ws, uint16_t* out, int H, int D, int S,
 hipError_t launch_probe(const void* src, size_t bytes, float* sink, int grid,
                         int unroll, hipStream_t stream);
 
+// Empty kernel of `grid` 256-thread groups (the launch-floor probe).
+hipError_t launch_empty(int grid, float* sink, hipStream_t stream);
+
 // Bit-exact quantizer (bits 8/4/3) over rows of D fp32 values.
 hipError_t launch_quantize(int bits, int G, const float* x, size_t rows, int D,
                            uint8_t* packed, uint16_t* scales, hipStream_t stream);

@@ -604,6 +604,41 @@ int va_fill_normal(float* x, size_t n, uint64_t seed, void* stream) {
     return VA_OK;
 }
 
+int va_probe_launch(int launches, double* us_per_launch) {
+    if (!us_per_launch) return fail(VA_ENULL, "us_per_launch is NULL");
+    if (launches < 1 || launches > 1000000) return fail(VA_EINVAL, "launches must be in [1, 10^6]");
+    *us_per_launch = 0.0;
+    float* sink = nullptr;
+    VA_HIP(hipMalloc(&sink, 4), "hipMalloc sink");
+    hipStream_t st = nullptr;
+    hipEvent_t e0 = nullptr, e1 = nullptr;
+    int rc = VA_OK;
+    do {
+        hipError_t e;
+        if ((e = hipStreamCreateWithFlags(&st, hipStreamNonBlocking)) != hipSuccess) { rc = hip_fail(e, "hipStreamCreate"); break; }
+        if ((e = hipEventCreate(&e0)) != hipSuccess || (e = hipEventCreate(&e1)) != hipSuccess) {
+            rc = hip_fail(e, "hipEventCreate");
+            break;
+        }
+        const int grid = cu_count() > 0 ? cu_count() : 256;
+        for (int i = 0; i < 50 && e == hipSuccess; ++i) e = va::launch_empty(grid, sink, st);
+        if (e == hipSuccess) e = hipStreamSynchronize(st);
+        if (e == hipSuccess) e = hipEventRecord(e0, st);
+        for (int i = 0; i < launches && e == hipSuccess; ++i) e = va::launch_empty(grid, sink, st);
+        if (e == hipSuccess) e = hipEventRecord(e1, st);
+        if (e == hipSuccess) e = hipEventSynchronize(e1);
+        float ms = 0.f;
+        if (e == hipSuccess) e = hipEventElapsedTime(&ms, e0, e1);
+        if (e != hipSuccess) { rc = hip_fail(e, "launch probe"); break; }
+        *us_per_launch = (double)ms * 1e3 / launches;
+    } while (0);
+    if (e0) (void)hipEventDestroy(e0);
+    if (e1) (void)hipEventDestroy(e1);
+    if (st) (void)hipStreamDestroy(st);
+    (void)hipFree(sink);
+    return rc;
+}
+
 int va_probe_read(size_t bytes, int reps, double* best_gbps) {
     if (!best_gbps) return fail(VA_ENULL, "best_gbps is NULL");
     if (bytes < (1u << 20) || reps < 1) return fail(VA_EINVAL, "probe needs >= 1 MiB and reps >= 1");
