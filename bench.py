@@ -443,8 +443,8 @@ def main() -> int:
     args = ap.parse_args()
 
     if args.gpus != 1:
-        log(f"bench.py: --gpus {args.gpus} is not supported: this build runs on one MI355X; "
-            f"the path shards by heads or by L (see DESIGN.md), run with --gpus 1")
+        log(f"bench.py: --gpus {args.gpus} is not supported: this build measures one MI355X "
+            f"(the decode step would shard by heads or by L across GPUs); run with --gpus 1")
         return 2
     if args.steps < 1:
         log("bench.py: --steps must be >= 1")
