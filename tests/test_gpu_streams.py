@@ -147,3 +147,129 @@ def test_more_streams_than_ticket_slots(inputs):
             o.free()
         for st in streams:
             st.destroy()
+
+
+class Job:
+    """One decode call with its own device inputs, enqueued on any stream into a
+    caller-provided (out, ws) pair: one-slot (tagged merge), grouped (counted
+    merge, matrix-core and vector-ALU forms) or paged (counted merge)."""
+
+    def __init__(self, kind, fmt, seed):
+        from tests import batch_util
+        self.kind, self.fmt, self.dev = kind, fmt, []
+        up = lambda a: self.dev.append(va.DeviceBuffer.from_array(a)) or self.dev[-1].ptr
+        D, G = 128, 32
+        if kind == "mha":
+            self.H, L = 6, 2500
+            c = gpu_util.case(va.fmt_bits(fmt), self.H, L, D, G, seed)
+            self.S = 5
+            self.bufs = dict(K=up(c["kpay"]), V=up(c["vpay"]), scK=up(c["ksc"]) if c["ksc"] is not None else 0,
+                             scV=up(c["vsc"]) if c["vsc"] is not None else 0, q=up(c["q"]))
+            self.launch_args = (self.H, L, D)
+            self.out_heads = self.H
+        elif kind == "gqa":
+            Hq, Hkv, L = 8, 2, 3000
+            kv = batch_util.kv_case(fmt, Hkv, L, D, G, seed)
+            q = batch_util.queries(Hq, D, seed + 1)
+            self.S = va.pick_splits_gqa(fmt, Hq, Hkv, L, D)
+            self.bufs = dict(K=up(kv["kpay"]), V=up(kv["vpay"]),
+                             scK=up(kv["ksc"]) if kv["ksc"] is not None else 0,
+                             scV=up(kv["vsc"]) if kv["vsc"] is not None else 0, q=up(q))
+            self.launch_args = (Hq, Hkv, L, D)
+            self.out_heads = Hq
+        else:
+            pb = batch_util.PagedBatch(fmt, [700, 1500, 64], 8, 2, D, G, 64, seed)
+            self.pb = pb
+            self.S = va.pick_splits_paged(fmt, pb.shape)
+            quant = pb.kspool is not None
+            self.bufs = dict(K=up(pb.kpool), V=up(pb.vpool), scK=up(pb.kspool) if quant else 0,
+                             scV=up(pb.vspool) if quant else 0, block_table=up(pb.table),
+                             seq_lens=up(pb.seq_lens), q=up(pb.q))
+            self.out_heads = len(pb.lens) * pb.Hq
+        self.D, self.G = D, G
+
+    def out_bytes(self):
+        return self.out_heads * self.D * 2
+
+    def ws_bytes(self):
+        return va.ws_bytes(self.out_heads, self.D, self.S)
+
+    def launch(self, out, ws, stream):
+        if self.kind == "paged":
+            b = va.PagedBufs(**self.bufs, out=out.ptr, ws=ws.ptr)
+            va.decode_paged(self.fmt, b, self.pb.shape, self.S, stream=stream)
+            return
+        b = va.DeviceBufs(**self.bufs, out=out.ptr, ws=ws.ptr)
+        if self.kind == "mha":
+            H, L, D = self.launch_args
+            va.launch(self.fmt, b, H, L, D, self.S, G=self.G, stream=stream)
+        else:
+            Hq, Hkv, L, D = self.launch_args
+            va.decode_gqa(self.fmt, b, Hq, Hkv, L, D, S=self.S, G=self.G, stream=stream)
+
+    def free(self):
+        for x in self.dev:
+            x.free()
+        if self.kind == "paged":
+            self.pb.free()
+
+
+def test_mixed_merge_protocols_on_concurrent_streams():
+    """One-slot (tagged) and grouped / paged (counted) calls interleaved on four
+    streams while a captured graph of all four replays on a fifth: every output
+    equals its single-stream result bit for bit, and no merge is lost."""
+    jobs = [Job("mha", va.Fmt.Q8M, 0x5A1), Job("gqa", va.Fmt.Q8M, 0x5A2),
+            Job("gqa", va.Fmt.F16M, 0x5A3), Job("paged", va.Fmt.Q4M, 0x5A4)]
+    assert all(j.S <= 64 for j in jobs)                       # all fused
+    NS = 4
+    streams = [va.Stream() for _ in range(NS)]
+    gstream = va.Stream()
+    pairs = {}                                                 # (owner, job) -> (out, ws)
+
+    def bufs(owner, k):
+        if (owner, k) not in pairs:
+            pairs[(owner, k)] = (va.DeviceBuffer(jobs[k].out_bytes()), va.DeviceBuffer(jobs[k].ws_bytes()))
+        return pairs[(owner, k)]
+
+    try:
+        eager = []
+        for k, j in enumerate(jobs):
+            out, ws = bufs("eager", k)
+            j.launch(out, ws, None)
+            va.sync()
+            eager.append(out.download(np.uint16))
+        for owner in ["graph"] + list(range(NS)):            # nothing is allocated under capture
+            for k in range(len(jobs)):
+                bufs(owner, k)
+        with va.Graph.capture(gstream) as cap:
+            for k, j in enumerate(jobs):
+                j.launch(*bufs("graph", k), gstream)
+        g = cap.graph
+        for rep in range(3):
+            for (owner, k), (out, _) in pairs.items():
+                if owner != "eager":
+                    out.zero()
+            va.sync()
+            print(f"mixed protocols rep {rep}: {NS} streams x {len(jobs)} jobs + a graph replay", flush=True)
+            for i in range(2):
+                for si, st in enumerate(streams):
+                    for k in range(len(jobs)):
+                        kk = (k + si) % len(jobs)                 # different job order per stream
+                        jobs[kk].launch(*bufs(si, kk), st)
+                if i == 0:
+                    g.launch(gstream)
+            for st in streams + [gstream]:
+                st.synchronize()
+            for (owner, k), (out, _) in pairs.items():
+                if owner != "eager":
+                    assert np.array_equal(out.download(np.uint16), eager[k]), (rep, owner, jobs[k].kind, jobs[k].fmt.label)
+        g.destroy()
+        assert va.merge_faults() == 0
+    finally:
+        for out, ws in pairs.values():
+            out.free()
+            ws.free()
+        for st in streams + [gstream]:
+            st.destroy()
+        for j in jobs:
+            j.free()
