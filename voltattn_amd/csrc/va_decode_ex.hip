@@ -27,7 +27,8 @@ namespace va {
 #define VA_EX_MODE 2
 #endif
 
-// Matrix-core form (va_mfma.hpp) for q8 and q4 rows with two or more query slots:
+// Matrix-core form (va_mfma.hpp) for q8 and q4 rows, and q3 rows at D = 128, with
+// two or more query slots:
 // MFMA_WAVES waves per work-group, 32-row wave tiles. A build with
 // VA_GQA_MFMA=0 runs the vector-ALU form of va_tiled.hpp for them instead (the
 // comparison variant the tests build; the product is built with the default).
@@ -41,22 +42,23 @@ constexpr int MFMA_WAVES = VA_MFMA_WAVES;
 constexpr int MFMA_TILE  = 32 * MFMA_WAVES;
 constexpr bool MFMA_ON   = VA_GQA_MFMA != 0;
 
-static bool mfma_kind(int kind) { return (kind == KQ8 || kind == KQ4) && MFMA_ON; }
-static bool mfma_form(int kind, int qg) { return mfma_kind(kind) && qg >= 2; }
+static bool mfma_kind(int kind, int D) { return (kind == KQ8 || kind == KQ4 || (kind == KQ3 && D == 128)) && MFMA_ON; }
+static bool mfma_form(int kind, int D, int qg) { return mfma_kind(kind, D) && qg >= 2; }
+template <int KIND, int D> constexpr bool mfma_kind_c = (KIND == KQ8 || KIND == KQ4 || (KIND == KQ3 && D == 128)) && MFMA_ON;
 
 // Query slots per work-group, per kind: the largest QG whose 8-wave form (two
 // waves per SIMD) fits in 256 VGPRs. Measured on MI355X (Hq/Hkv = 32/8, 64/8,
 // 28/4 at L = 16K-64K): QG = 4 at two waves per SIMD beats QG = 8 at one for
 // f16 and q8 (groups of 8 run as two sub-groups, 12-38% faster), and q4 is
 // fastest at QG = 2 (QG = 4 spills at two waves per SIMD). The matrix-core
-// form carries 4 slots for q4 too. A build with VA_EX_QMAX = 1|2|4 lowers the
-// cap (a tuning variant).
+// form carries 4 slots for q4, and for q3 at D = 128, too. A build with
+// VA_EX_QMAX = 1|2|4 lowers the cap (a tuning variant).
 #ifndef VA_EX_QMAX
 #define VA_EX_QMAX 0
 #endif
-int max_query_slots(int kind) {
+int max_query_slots(int kind, int D) {
     constexpr int cap = VA_EX_QMAX;
-    const int q = (kind == KF16 || kind == KQ8 || mfma_kind(kind)) ? 4 : 2;
+    const int q = (kind == KF16 || kind == KQ8 || mfma_kind(kind, D)) ? 4 : 2;
     return (cap == 1 || cap == 2 || cap == 4) ? std::min(q, cap) : q;
 }
 
@@ -87,8 +89,8 @@ static int minb_of(int qg) {
     }
 }
 
-int ex_groups_per_cu(int kind, int qg) {
-    if (mfma_form(kind, qg)) return 1;
+int ex_groups_per_cu(int kind, int D, int qg) {
+    if (mfma_form(kind, D, qg)) return 1;
     switch (kind) {
         case KF16: return minb_of<KF16>(qg);
         case KQ8:  return minb_of<KQ8>(qg);
@@ -122,17 +124,17 @@ int tile_positions_ex(int kind, int D) {
         case KF16: return D == 128 ? max_tile<KF16, 128>() : max_tile<KF16, 64>();
         case KQ8:  return std::max(MFMA_TILE, D == 128 ? max_tile<KQ8, 128>() : max_tile<KQ8, 64>());
         case KQ4:  return std::max(MFMA_TILE, D == 128 ? max_tile<KQ4, 128>() : max_tile<KQ4, 64>());
-        default:   return D == 128 ? max_tile<KQ3, 128>()  : max_tile<KQ3, 64>();
+        default:   return D == 128 ? std::max(MFMA_ON ? MFMA_TILE : 1, max_tile<KQ3, 128>()) : max_tile<KQ3, 64>();
     }
 }
 
 template <int KIND, int D, int G, int QG, bool PAGED>
 static hipError_t launch_ex(int groups, const DecodeArgs& a, hipStream_t st) {
-    if constexpr ((KIND == KQ8 || KIND == KQ4) && QG >= 2 && MFMA_ON) {
+    if constexpr (mfma_kind_c<KIND, D> && QG >= 2) {
         hipLaunchKernelGGL((decode_mfma<KIND, D, G, MFMA_WAVES, QG, PAGED>),
                            dim3((unsigned)(groups * a.S)), dim3(MFMA_WAVES * 64), 0, st, a);
         return hipGetLastError();
-    } else if constexpr (KIND == KQ4 && QG > 2) {
+    } else if constexpr ((KIND == KQ4 || KIND == KQ3) && QG > 2) {
         return hipErrorInvalidValue;                 // matrix-core form only
     } else {
         using Cfg = ExCfg<KIND, QG>;
@@ -152,9 +154,10 @@ static hipError_t launch_qg(int qg, int groups, const DecodeArgs& a, hipStream_t
             else return hipErrorInvalidValue;       // QG = 1 contiguous: va_decode.hip
         case 2: return launch_ex<KIND, D, G, 2, PAGED>(groups, a, st);
         case 4:
-            if constexpr (KIND == KF16 || KIND == KQ8 || KIND == KQ4) return launch_ex<KIND, D, G, 4, PAGED>(groups, a, st);
+            if constexpr (KIND == KF16 || KIND == KQ8 || KIND == KQ4 || (KIND == KQ3 && D == 128))
+                return launch_ex<KIND, D, G, 4, PAGED>(groups, a, st);
             else return hipErrorInvalidValue;
-        default: return hipErrorInvalidValue;          // above max_query_slots(kind)
+        default: return hipErrorInvalidValue;          // above max_query_slots(kind, D)
     }
 }
 

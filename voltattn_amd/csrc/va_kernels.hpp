@@ -71,16 +71,16 @@ hipError_t launch_decode(int kind, bool tiled, int H, int D, int G,
 
 // Grouped-query and paged forms of the tiled kernels (va_decode_ex.hip).
 // groups = merge groups (B * hkv * nsub); qg = query slots per work-group
-// (max_query_slots(kind) at most); paged selects the block-table form.
+// (max_query_slots(kind, D) at most); paged selects the block-table form.
 hipError_t launch_decode_ex(int kind, int D, int G, int qg, bool paged, int groups,
                             const DecodeArgs& a, hipStream_t stream);
 
 // Largest query-slot count (QG) a work-group of the kind carries, and the
 // work-group tile (positions per iteration) of the grouped/paged kernels.
-int max_query_slots(int kind);
+int max_query_slots(int kind, int D);
 int tile_positions_ex(int kind, int D);
 // Work-groups per CU the grouped/paged launch of (kind, QG) is built for.
-int ex_groups_per_cu(int kind, int qg);
+int ex_groups_per_cu(int kind, int D, int qg);
 
 // Work-groups per CU the split rule aims for (tiled kernels: the configured
 // groups per CU of the kind; naive kernels: 8).

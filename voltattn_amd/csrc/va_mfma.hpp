@@ -1,7 +1,7 @@
 // va_mfma.hpp — grouped-query decode on the matrix cores (gfx950 MFMA).
 //
-// Same partials as decode_tiled (va_tiled.hpp), for the q8 rows, with q.K and
-// P.V as v_mfma_f32_16x16x32_f16 products instead of per-lane dot/axpy chains
+// Same partials as decode_tiled (va_tiled.hpp), for q8 and q4 rows and q3 rows at
+// D = 128, with q.K and P.V on the matrix cores instead of per-lane dot/axpy chains
 // (the VALU form spends ~28 vector instructions per position at four query
 // heads; here the matrix core does the multiply-adds and the VALU keeps the
 // unpack, the softmax and the operand set-up).
@@ -96,26 +96,60 @@ __device__ __forceinline__ f16x8 q8_to_f16x8(uint32_t w0, uint32_t w1, uint32_t 
     return f16x8{p0.x, p0.y, p1.x, p1.y, p2.x, p2.y, p3.x, p3.y};
 }
 
+// 8 q3 codes n = v + 4 (two dwords of bytes, byte order) -> 8 exact fp16 values v.
+__device__ __forceinline__ f16x8 q3b_to_f16x8(uint32_t w0, uint32_t w1, uint32_t magic) {
+    const h2 bias = hh(1028.f, 1028.f);
+    const h2 p0 = as_h2(__builtin_amdgcn_perm(magic, w0, 0x04010400u)) - bias;
+    const h2 p1 = as_h2(__builtin_amdgcn_perm(magic, w0, 0x04030402u)) - bias;
+    const h2 p2 = as_h2(__builtin_amdgcn_perm(magic, w1, 0x04010400u)) - bias;
+    const h2 p3 = as_h2(__builtin_amdgcn_perm(magic, w1, 0x04030402u)) - bias;
+    return f16x8{p0.x, p0.y, p1.x, p1.y, p2.x, p2.y, p3.x, p3.y};
+}
+
+// Four 3-bit codes in bits 0..11 of x (code i at bit 3i) -> one code per byte:
+// the upper pair moves up by 10 (to bits 16 and 19), then every odd code by 5.
+__device__ __forceinline__ uint32_t q3_spread4(uint32_t x) {
+    const uint32_t t = (x | (x << 10)) & 0x003F003Fu;
+    return (t | (t << 5)) & 0x07070707u;
+}
+
+// The 32 codes of a 12-byte q3 chunk (code e at bits [3e, 3e + 3) of the
+// little-endian 96-bit word) -> 32 bytes in code order, byte e = code e.
+__device__ __forceinline__ void q3_to_bytes(const u32x4& w, uint32_t (&b)[8]) {
+    b[0] = q3_spread4(__builtin_amdgcn_ubfe(w.x, 0, 12));
+    b[1] = q3_spread4(__builtin_amdgcn_ubfe(w.x, 12, 12));
+    b[2] = q3_spread4(__builtin_amdgcn_alignbit(w.y, w.x, 24) & 0xFFFu);
+    b[3] = q3_spread4(__builtin_amdgcn_ubfe(w.y, 4, 12));
+    b[4] = q3_spread4(__builtin_amdgcn_ubfe(w.y, 16, 12));
+    b[5] = q3_spread4(__builtin_amdgcn_alignbit(w.z, w.y, 28) & 0xFFFu);
+    b[6] = q3_spread4(__builtin_amdgcn_ubfe(w.z, 8, 12));
+    b[7] = q3_spread4(w.z >> 20);
+}
+
 template <int KIND, int D, int G, int WAVES, int QG, bool PAGED>
 __global__ __launch_bounds__(WAVES * 64, 1) void decode_mfma(DecodeArgs a) {
-    static_assert(KIND == KQ8 || KIND == KQ4, "matrix-core form: q8 and q4 rows");
+    static_assert(KIND == KQ8 || KIND == KQ4 || (KIND == KQ3 && D == 128),
+                  "matrix-core form: q8 and q4 rows, and q3 rows at D = 128");
     constexpr bool Q4  = KIND == KQ4;
-    constexpr int ROWB = Q4 ? D / 2 : D;         // bytes per row
+    constexpr bool Q3  = KIND == KQ3;
+    constexpr int ROWB = Q3 ? 3 * D / 8 : Q4 ? D / 2 : D;   // bytes per row in memory
+    constexpr int VRB  = Q3 ? D : ROWB;          // bytes per staged V row (q3: a byte per code)
     constexpr int NG   = D / G;                  // scale groups per row (1, 2, 4)
     constexpr int QP   = 16 / NG;                // column slots per scale group
     static_assert(QG >= 1 && QG <= QP, "query slots per work-group");
     constexpr int TW   = 32;                     // rows per wave tile (two 16-row blocks)
     constexpr int TB   = TW * WAVES;
     constexpr int DQ   = ROWB / 4;               // row bytes per lane quarter (A operand)
-    constexpr int KL   = DQ >= 16 ? DQ / 16 : 1; // K loads per block per lane (16 B; q4 at D = 64: 8 B)
+    constexpr int KL   = Q3 ? 1 : DQ >= 16 ? DQ / 16 : 1;   // K loads per block per lane (16 B; q4 at D = 64: 8 B; q3: 12 B)
     constexpr int NJ   = D / 64;                 // q.K MFMAs (k = 64) per block and digit
     constexpr int NB   = D / 16;                 // P.V column blocks (16 dimensions each)
-    constexpr int NC   = ROWB / 16;              // 16-byte column chunks of a V row
-    constexpr int VL   = TW * ROWB / (64 * 16);  // 16-byte V loads per lane per tile
-    constexpr int VSTR = ROWB + 16;              // LDS row stride of the staged V tile
+    constexpr int NC   = VRB / 16;               // 16-byte column chunks of a staged V row
+    constexpr int VCH  = Q3 ? 12 : 16;           // bytes per V load per lane (q3: a quarter row)
+    constexpr int VL   = TW * ROWB / (64 * VCH); // V loads per lane per tile
+    constexpr int VSTR = VRB + 16;               // LDS row stride of the staged V tile
     constexpr int VROWS = TW + 4;                // rows 16..31 sit 4 slots further
     constexpr int SCE  = NG >= 2 ? TW * NG / 2 : TW;   // scale words (dwords, or halves at NG = 1)
-    static_assert(VL >= 1 && SCE <= 64 && (Q4 ? NC * 2 == NB : (NC == NB && NJ == KL)), "tile shape");
+    static_assert(VL >= 1 && SCE <= 64 && (Q4 ? NC * 2 == NB : (NC == NB && (Q3 || NJ == KL))), "tile shape");
 
     __shared__ __align__(16) uint8_t  s_v[WAVES][VROWS * VSTR];
     __shared__ __align__(16) uint32_t s_sc[WAVES][NG][TW];   // (k | v << 16) scale pairs
@@ -218,7 +252,10 @@ __global__ __launch_bounds__(WAVES * 64, 1) void decode_mfma(DecodeArgs a) {
             for (int c = 0; c < 2; ++c)
 #pragma unroll
                 for (int i = 0; i < KL; ++i) {
-                    if constexpr (DQ >= 16) {
+                    if constexpr (Q3) {
+                        const u32x3 w = ld96(tk, koff + (uint32_t)(c * 16 * ROWB), tpos * ROWB);
+                        kk[c][i] = u32x4{w.x, w.y, w.z, 0u};
+                    } else if constexpr (DQ >= 16) {
                         kk[c][i] = ld128(tk, koff + (uint32_t)(c * 16 * ROWB + 16 * i), tpos * ROWB);
                     } else {
                         const u32x2 h = ld64(tk, koff + (uint32_t)(c * 16 * ROWB), tpos * ROWB);
@@ -226,8 +263,14 @@ __global__ __launch_bounds__(WAVES * 64, 1) void decode_mfma(DecodeArgs a) {
                     }
                 }
 #pragma unroll
-            for (int i = 0; i < VL; ++i)
-                vv[i] = ld128(tv, (uint32_t)(16 * (64 * i + lane)), tpos * ROWB);
+            for (int i = 0; i < VL; ++i) {
+                if constexpr (Q3) {
+                    const u32x3 w = ld96(tv, (uint32_t)(12 * (64 * i + lane)), tpos * ROWB);
+                    vv[i] = u32x4{w.x, w.y, w.z, 0u};
+                } else {
+                    vv[i] = ld128(tv, (uint32_t)(16 * (64 * i + lane)), tpos * ROWB);
+                }
+            }
             __builtin_amdgcn_sched_barrier(0);
         };
 
@@ -302,11 +345,11 @@ __global__ __launch_bounds__(WAVES * 64, 1) void decode_mfma(DecodeArgs a) {
 #pragma unroll
                 for (int k = 0; k < 3; ++k) qd[k][j] = u32x4{bq[k][0], bq[k][1], bq[k][2], bq[k][3]};
             }
-            if constexpr (Q4) {                   // codes enter as n = v + 8
+            if constexpr (Q4 || Q3) {             // codes enter as n = v + 8 (q4), v + 4 (q3)
 #pragma unroll
                 for (int k = 0; k < 3; ++k) {
                     const float cs = rows_sum(dsum[k]);
-                    qoff[k] = -8 * (int)cs;
+                    qoff[k] = (Q4 ? -8 : -4) * (int)cs;
                 }
             }
         }
@@ -336,8 +379,17 @@ __global__ __launch_bounds__(WAVES * 64, 1) void decode_mfma(DecodeArgs a) {
 #pragma unroll
             for (int i = 0; i < VL; ++i) {
                 const int chunk = 64 * i + lane;
-                const int row = chunk / (ROWB / 16), c16 = chunk % (ROWB / 16);
-                *reinterpret_cast<u32x4*>(sv_w + (row + 4 * (row >> 4)) * VSTR + 16 * c16) = vv[i];
+                if constexpr (Q3) {               // a quarter row of codes -> 32 bytes
+                    const int row = chunk >> 2, qtr = chunk & 3;
+                    uint32_t bt[8];
+                    q3_to_bytes(vv[i], bt);
+                    uint8_t* dst = sv_w + (row + 4 * (row >> 4)) * VSTR + 32 * qtr;
+                    *reinterpret_cast<u32x4*>(dst)      = u32x4{bt[0], bt[1], bt[2], bt[3]};
+                    *reinterpret_cast<u32x4*>(dst + 16) = u32x4{bt[4], bt[5], bt[6], bt[7]};
+                } else {
+                    const int row = chunk / (ROWB / 16), c16 = chunk % (ROWB / 16);
+                    *reinterpret_cast<u32x4*>(sv_w + (row + 4 * (row >> 4)) * VSTR + 16 * c16) = vv[i];
+                }
             }
             // scales -> LDS as (k | v << 16) pairs, [group][row]
             if (lane < SCE) {
@@ -358,12 +410,19 @@ __global__ __launch_bounds__(WAVES * 64, 1) void decode_mfma(DecodeArgs a) {
             for (int k = 0; k < 3; ++k)
 #pragma unroll
                 for (int c = 0; c < 2; ++c) acc[k][c] = i32x4{qoff[k], qoff[k], qoff[k], qoff[k]};
+            uint32_t kb3[2][8];                   // q3: the codes of each block as bytes
+            if constexpr (Q3) {
+#pragma unroll
+                for (int c = 0; c < 2; ++c) q3_to_bytes(kk[c][0], kb3[c]);
+            }
 #pragma unroll
             for (int j = 0; j < NJ; ++j)
 #pragma unroll
                 for (int c = 0; c < 2; ++c) {
                     u32x4 kop;                    // A operand: int8 codes of 16 k slots
-                    if constexpr (!Q4) {
+                    if constexpr (Q3) {
+                        kop = u32x4{kb3[c][4 * j], kb3[c][4 * j + 1], kb3[c][4 * j + 2], kb3[c][4 * j + 3]};
+                    } else if constexpr (!Q4) {
                         kop = kk[c][j];
                     } else if constexpr (D == 128) {
                         kop = j == 0 ? (kk[c][0] & 0x0F0F0F0Fu) : ((kk[c][0] >> 4) & 0x0F0F0F0Fu);
@@ -380,7 +439,8 @@ __global__ __launch_bounds__(WAVES * 64, 1) void decode_mfma(DecodeArgs a) {
 #pragma unroll
             for (int c16 = 0; c16 < NC; ++c16) {
                 const i32x2 t = __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_i32x2*)(sv_w + vrd + 16 * c16));
-                if constexpr (!Q4) vf[c16] = q8_to_f16x8((uint32_t)t[0], (uint32_t)t[1], magic);
+                if constexpr (Q3) vf[c16] = q3b_to_f16x8((uint32_t)t[0], (uint32_t)t[1], magic);
+                else if constexpr (!Q4) vf[c16] = q8_to_f16x8((uint32_t)t[0], (uint32_t)t[1], magic);
                 else q4_to_f16x8((uint32_t)t[0], (uint32_t)t[1], magic, vf[2 * c16], vf[2 * c16 + 1]);
             }
             // scale pairs of this lane's 8 positions (16c + 4g + v), group cg

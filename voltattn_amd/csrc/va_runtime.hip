@@ -325,8 +325,8 @@ int  log2i(int x) { int s = 0; while ((1 << s) < x) ++s; return s; }
 // Query slots per work-group (QG, a power of two) and sub-groups per KV head:
 // as few sub-groups as the kind's slot limit allows (each re-reads the rows),
 // then the smallest QG that covers the group.
-void pick_qg(int kind, int qgroup, int* qg, int* nsub) {
-    const int qmax = va::max_query_slots(kind);
+void pick_qg(int kind, int D, int qgroup, int* qg, int* nsub) {
+    const int qmax = va::max_query_slots(kind, D);
     const int ns = (qgroup + qmax - 1) / qmax;
     const int per = (qgroup + ns - 1) / ns;
     int q = 1;
@@ -342,7 +342,7 @@ void pick_qg(int kind, int qgroup, int* qg, int* nsub) {
 void splits_ex(int kind, int D, int qg, int groups, int max_len, int S_req, int* S, int* chunk) {
     int cus = cu_count();
     if (cus <= 0) cus = 256;
-    cus *= va::ex_groups_per_cu(kind, qg);
+    cus *= va::ex_groups_per_cu(kind, D, qg);
     const int tb = va::tile_positions_ex(kind, D);
     const int tiles = std::max(1, (max_len + tb - 1) / tb);
     int s0 = S_req;
@@ -382,7 +382,7 @@ int va_pick_splits_gqa(va_fmt fmt, int Hq, int Hkv, int L, int D, int* S) {
     if (Hq == Hkv) return va_pick_splits(fmt, Hq, L, D, S);
     if (!tiled_of(fmt)) return fail(VA_EINVAL, "grouped-query decode needs a tiled format (f16+, q8+, q4+, q3+)");
     int qg, nsub, chunk;
-    pick_qg(kind_of(fmt), Hq / Hkv, &qg, &nsub);
+    pick_qg(kind_of(fmt), D, Hq / Hkv, &qg, &nsub);
     splits_ex(kind_of(fmt), D, qg, Hkv * nsub, L, 0, S, &chunk);
     return VA_OK;
 }
@@ -405,7 +405,7 @@ int va_decode_gqa(va_fmt fmt, const va_bufs* b, int Hq, int Hkv, int L, int D, i
     int rc = validate(fmt, b, Hkv, L, D, G, 1, true);
     if (rc) return rc;
     int qg, nsub, Sx, chunk;
-    pick_qg(kind_of(fmt), Hq / Hkv, &qg, &nsub);
+    pick_qg(kind_of(fmt), D, Hq / Hkv, &qg, &nsub);
     const int groups = Hkv * nsub;
     splits_ex(kind_of(fmt), D, qg, groups, L, S, &Sx, &chunk);
     if ((long long)Hq * Sx > 0x7FFFFFFFLL || (long long)groups * Sx > 0x7FFFFFFFLL)
@@ -474,7 +474,7 @@ int va_pick_splits_paged(va_fmt fmt, const va_paged_shape* sh, int* S) {
     int rc = validate_shape(fmt, sh, true);
     if (rc) return rc;
     int qg, nsub, chunk;
-    pick_qg(kind_of(fmt), sh->Hq / sh->Hkv, &qg, &nsub);
+    pick_qg(kind_of(fmt), sh->D, sh->Hq / sh->Hkv, &qg, &nsub);
     splits_ex(kind_of(fmt), sh->D, qg, sh->B * sh->Hkv * nsub, std::max(1, sh->max_seq_len), 0, S, &chunk);
     // a split may span at most MAX_SPLIT_PAGES pages
     while ((chunk / sh->page_rows) + 2 > va::MAX_SPLIT_PAGES && *S < 0x7FFF) {
@@ -505,7 +505,7 @@ int va_decode_paged(va_fmt fmt, const va_paged_bufs* b, const va_paged_shape* sh
             return fail(VA_EALIGN, "sk and sv must be %zu-byte aligned", sal);
     }
     int qg, nsub, Sx, chunk;
-    pick_qg(kind_of(fmt), sh->Hq / sh->Hkv, &qg, &nsub);
+    pick_qg(kind_of(fmt), sh->D, sh->Hq / sh->Hkv, &qg, &nsub);
     const long long groups = (long long)sh->B * sh->Hkv * nsub;
     if (S == 0) {
         rc = va_pick_splits_paged(fmt, sh, &Sx);
