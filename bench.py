@@ -517,7 +517,7 @@ def main() -> int:
         # definition (K+V payload + scales actually read), tok/s per decode step.
         min_set = int(args.set_gib * 2**30)
         specs = [("gqa", "q8+", dict(Hq=32, Hkv=8, L=65536)), ("gqa", "f16+", dict(Hq=32, Hkv=8, L=65536)),
-                 ("gqa", "q4+", dict(Hq=32, Hkv=8, L=65536)),
+                 ("gqa", "q4+", dict(Hq=32, Hkv=8, L=65536)), ("gqa", "q3+", dict(Hq=32, Hkv=8, L=65536)),
                  ("paged", "q8+", dict(B=8, Hq=32, Hkv=8, L=16384, P=256)),
                  ("paged", "q8+", dict(B=1, Hq=32, Hkv=32, L=16384, P=256))]
         for kind, name, p in specs:
