@@ -35,8 +35,9 @@ Method (reference bench, src/voltattn.cu:967-1070, re-derived for MI355X):
     kernel's mean launch time (the K back-to-back steps between events: one
     launch per step); the split pass alone (va_decode_splits) beside it;
   * launch floor (va_probe_launch): us per back-to-back launch of an empty
-    kernel with the decode step's grid, the fixed cost every step pays
-    outside its own work (reported as launch_floor_us);
+    kernel with the decode step's grid (reported as launch_floor_us); an
+    upper bound on the per-step launch cost, since part of it overlaps a
+    running kernel;
   * cpu_baseline: the oracle's double-precision reference attention
     (reference(), src/voltattn.cu:769-794) on the headline shape, timed on
     this host (rank 0, N=1 only); `cpu_configs0` is the same on configs[0]
