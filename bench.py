@@ -454,7 +454,7 @@ def main() -> int:
     import voltattn_amd as va
     info = va.device_info()
     log(f"device: {info['name']} {info['arch']} CUs={info['compute_units']} "
-        f"mem={info['total_mem'] / 2**30:.0f} GiB")
+        f"mem={info['total_mem'] / 2**30:.0f} GiB; library {va.LIB_PATH}")
     ceiling = va.probe_read(int(args.probe_gib * 2**30), reps=5)
     log(f"probed read ceiling: {ceiling:.1f} GB/s ({args.probe_gib:g} GiB buffer)")
     launch_floor = va.probe_launch(2000)
@@ -520,6 +520,8 @@ def main() -> int:
         specs = [("gqa", "q8+", dict(Hq=32, Hkv=8, L=65536)), ("gqa", "f16+", dict(Hq=32, Hkv=8, L=65536)),
                  ("gqa", "q4+", dict(Hq=32, Hkv=8, L=65536)), ("gqa", "q3+", dict(Hq=32, Hkv=8, L=65536)),
                  ("paged", "q8+", dict(B=8, Hq=32, Hkv=8, L=16384, P=256)),
+                 ("paged", "q4+", dict(B=8, Hq=32, Hkv=8, L=16384, P=256)),
+                 ("paged", "q3+", dict(B=8, Hq=32, Hkv=8, L=16384, P=256)),
                  ("paged", "q8+", dict(B=1, Hq=32, Hkv=32, L=16384, P=256))]
         for kind, name, p in specs:
             fmt = va.Fmt.parse(name)
