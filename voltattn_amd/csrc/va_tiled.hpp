@@ -298,7 +298,9 @@ __global__ __launch_bounds__(WAVES * 64, MINB) void decode_tiled(
         // work-group). Loads past the end of the split return zeros without
         // memory traffic, so the prefetch after the last tile adds no traffic.
         // (An exit inside the loop instead measured 1.5 us slower for the paged
-        // one-slot form: it changes how the loop body is scheduled.)
+        // one-slot form, and skipping the last prefetch with a uniform test made
+        // q4+ at H=32 L=16384 1.7 us slower: both change how the loop body is
+        // scheduled.)
         const int npair = niter / 2;
         // f16 rows in 8-wave groups: the older wave of each SIMD pair wins issue
         // and runs ahead, and the younger one finishes alone with half the loads
