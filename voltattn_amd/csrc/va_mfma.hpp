@@ -159,6 +159,7 @@ __global__ __launch_bounds__(WAVES * 64, 1) void decode_mfma(DecodeArgs a) {
     __shared__ float s_acc[QG][D];
     __shared__ float s_mf[QG], s_lf[QG];
     __shared__ int   s_page[PAGED ? MAX_SPLIT_PAGES : 1];
+    __shared__ int   s_prog[WAVES];                         // tile pair each wave is on (issue priority)
 
     // ---- work-group -> (sequence b, KV head hk, query sub-group, split s)
     Route rt;
@@ -526,15 +527,34 @@ __global__ __launch_bounds__(WAVES * 64, 1) void decode_mfma(DecodeArgs a) {
 
         // Tiles in pairs; an odd count leaves after its last tile (niter is
         // uniform over the work-group; the prefetch past the split reads nothing).
+        //
+        // q4 and q3 rows keep both waves of a SIMD (waves w and w ^ 4 under the
+        // dispatcher's round-robin placement) busy on the vector ALU, and the
+        // older one wins issue: it runs ahead, and the other finishes alone with
+        // half the loads in flight. Each wave posts its tile pair in LDS and
+        // takes issue priority while it trails its partner (a stale entry left
+        // by an earlier group changes one pair's priority, nothing else).
+        // Measured on MI355X, Hq 32 / Hkv 8, 7 interleaved rounds: L 65536 q4+
+        // 24.5 -> 24.3 us, q3+ 28.6 -> 28.3 us; paged B 8 x 16384 q4+ 45.6 ->
+        // 43.5 us. q8 rows lose ~0.2 us with it and keep free issue.
+        constexpr bool PRIO = WAVES == 8 && (KIND == KQ4 || KIND == KQ3);
         const int npair = (niter + 1) / 2;
         for (int ip = 0; ip < npair; ++ip) {
             const int it = 2 * ip;
+            if constexpr (PRIO) {
+                __hip_atomic_store(&s_prog[wave], ip + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+                const int other = uniform(__hip_atomic_load(&s_prog[wave ^ 4], __ATOMIC_RELAXED,
+                                                            __HIP_MEMORY_SCOPE_WORKGROUP));
+                if (other > ip + 1) __builtin_amdgcn_s_setprio(2);
+                else __builtin_amdgcn_s_setprio(0);
+            }
             load_tile(it + 1, kb, vb, skb, svb);
             compute_tile(it, ka, va_, ska, sva);
             if (it + 1 >= niter) break;
             load_tile(it + 2, ka, va_, ska, sva);
             compute_tile(it + 1, kb, vb, skb, svb);
         }
+        if constexpr (PRIO) __builtin_amdgcn_s_setprio(0);
     }
 
     // ---- work-group merge. Per query slot q: lsum of column q summed over the
