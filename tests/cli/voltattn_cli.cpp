@@ -570,6 +570,7 @@ int bench(int G, const std::vector<int>& Ls, const std::vector<Fmt>& fmts, int r
     }
     if (!json_path.empty()) {
         std::ofstream js(json_path);
+        js.precision(17);                                    // figures round-trip exactly
         js << "{\"device\": \"" << info.arch << "\", \"ceiling_gbps\": " << ceil_gbs << ", \"G\": " << G
            << ", \"rows\": [";
         for (size_t i = 0; i < rows.size(); ++i) {
