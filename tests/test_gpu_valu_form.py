@@ -1,10 +1,11 @@
-"""GPU: the vector-ALU form of grouped and paged q8+/q4+ decode.
+"""GPU: the vector-ALU form of grouped and paged q8+/q4+ decode, and of q3+ at D = 128.
 
 The product runs these on the matrix cores; the vector-ALU kernels are built
 into a comparison library (build/variants/libvoltattn_hip_valu.so, compiled
 with VA_GQA_MFMA=0), so the cases run in one child process that loads it
 (tests/variant_pkg.py): grouped-query decode (four query slots per work-group
-for q8+, two for q4+, sub-groups and masked slots) at D = 128 and 64 and
+for q8+, two for q4+ and q3+, sub-groups and masked slots) at D = 128 and 64
+(q3+: D = 128, the only width it runs on the matrix cores in the product) and
 G = 32 and 64, and paged batches with ragged lengths, each against the
 oracle's double reference (oracle.batch) within the reference's gate
 (src/voltattn.cu:903) and the fp16 rounding bound. The matrix-core form of the
@@ -16,7 +17,7 @@ import pytest
 
 ROOT = Path(__file__).resolve().parent.parent
 pytestmark = pytest.mark.gpu
-N_CASES = 26
+N_CASES = 36
 
 
 def _child() -> None:
@@ -40,8 +41,10 @@ def _child() -> None:
     shapes = [(Hq, Hkv, L, 128, 32) for Hq, Hkv in ((8, 2), (12, 4), (16, 2), (6, 3)) for L in (257, 3000)]
     # other scale layouts: one scale group per lane row (D = 64, G = 64), two (D = 128, G = 64)
     shapes += [(8, 2, 3000, 64, 32), (12, 4, 1000, 64, 64), (8, 2, 2000, 128, 64), (6, 3, 777, 64, 32)]
-    for fmt in (va.Fmt.Q8M, va.Fmt.Q4M):
+    for fmt in (va.Fmt.Q8M, va.Fmt.Q4M, va.Fmt.Q3M):
         for Hq, Hkv, L, D, G in shapes:
+            if fmt == va.Fmt.Q3M and D != 128:
+                continue
             print(f"valu gqa {fmt.label} Hq={Hq} Hkv={Hkv} L={L} D={D} G={G}", flush=True)
             seed = 0x7A1 + Hq * 31 + L
             c = batch_util.kv_case(fmt, Hkv, L, D, G, seed)
