@@ -166,15 +166,18 @@ int va_f32_to_f16(const float* x, size_t n, uint16_t* out, void* stream);
 int va_fill_normal(float* x, size_t n, uint64_t seed, void* stream);
 
 /* Empirical HBM read ceiling: best GB/s over `reps` timed reads of a
- * `bytes`-sized device buffer, taking the best of several launch shapes
- * (probe_ceiling + read_kernel, src/voltattn.cu:64-78, 935-957). */
+ * `bytes`-sized device buffer, taking the best of several launch shapes: a
+ * grid-stride read (the reference's form, probe_ceiling + read_kernel,
+ * src/voltattn.cu:64-78, 935-957) and a chunked read (each work-group streams
+ * one contiguous chunk, the shape of a decode split; buffers of 16 MiB and up). */
 int va_probe_read(size_t bytes, int reps, double* best_gbps);
 
 /* Launch floor: microseconds per launch of an empty kernel with one 256-thread
  * work-group per CU (the decode step's grid at H*S = CUs), `launches` of them
- * back to back on a private stream after a warm-up: the fixed cost each decode
- * step pays outside its own work. No counterpart in the reference (its bench
- * reports only the read ceiling); a measurement aid like va_probe_read. */
+ * back to back on a private stream after a warm-up: an upper bound on the
+ * launch cost a decode step pays outside its own work (part of it overlaps a
+ * running kernel). No counterpart in the reference (its bench reports only the
+ * read ceiling); a measurement aid like va_probe_read. */
 int va_probe_launch(int launches, double* us_per_launch);
 
 /* ---- grouped-query attention, batches and paged caches ----

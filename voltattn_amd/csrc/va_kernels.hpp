@@ -105,6 +105,12 @@ hipError_t launch_merge(const float* ws, uint16_t* out, int H, int D, int S,
 hipError_t launch_probe(const void* src, size_t bytes, float* sink, int grid,
                         int unroll, hipStream_t stream);
 
+// Chunked read probe: `grid` work-groups, each streaming a contiguous chunk of
+// whole 4096*unroll-byte tiles (unroll 4 or 8); the bytes it reads (a multiple
+// of grid * tile, at most `bytes`) go to *bytes_read.
+hipError_t launch_probe_chunks(const void* src, size_t bytes, float* sink, int grid, int unroll,
+                               hipStream_t stream, size_t* bytes_read);
+
 // Empty kernel of `grid` 256-thread groups (the launch-floor probe).
 hipError_t launch_empty(int grid, float* sink, hipStream_t stream);
 

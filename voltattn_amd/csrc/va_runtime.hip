@@ -676,6 +676,24 @@ int va_probe_read(size_t bytes, int reps, double* best_gbps) {
             }
             if (e != hipSuccess) break;
         }
+        // the chunked form: one or two 4-wave groups per CU, 4 or 8 loads per lane in flight
+        for (int gpc = 1; gpc <= 2 && e == hipSuccess; ++gpc) {
+            for (int un : unrolls) {
+                if (bytes / ((size_t)4096 * un) / (size_t)(cus * gpc) == 0) continue;   // buffer too small
+                size_t nread = 0;
+                if ((e = va::launch_probe_chunks(src, bytes, sink, cus * gpc, un, nullptr, &nread)) != hipSuccess) break;
+                for (int r = 0; r < reps && e == hipSuccess; ++r) {
+                    (void)hipEventRecord(e0, nullptr);
+                    e = va::launch_probe_chunks(src, bytes, sink, cus * gpc, un, nullptr, &nread);
+                    (void)hipEventRecord(e1, nullptr);
+                    if (e == hipSuccess) e = hipEventSynchronize(e1);
+                    float ms = 0.f;
+                    if (e == hipSuccess) e = hipEventElapsedTime(&ms, e0, e1);
+                    if (e == hipSuccess && ms > 0.f) best = std::max(best, (double)nread / (ms * 1e6));
+                }
+                if (e != hipSuccess) break;
+            }
+        }
         if (e != hipSuccess) rc = hip_fail(e, "probe");
     } while (0);
     if (e0) (void)hipEventDestroy(e0);
