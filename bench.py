@@ -16,7 +16,9 @@ and tok/s; `formats` repeats the L=16384 rows by format.
 
 Method (reference bench, src/voltattn.cu:967-1070, re-derived for MI355X):
   * read ceiling: a >= 4 GiB buffer (16x the 256 MB Infinity Cache) read with
-    128-bit loads, best over launch shapes (va_probe_read);
+    128-bit non-temporal loads, best over launch shapes of two forms, the
+    reference's grid-stride read and a chunked read (one contiguous chunk per
+    work-group, the shape of a decode split) (va_probe_read);
   * K/V are drawn N(0,1) on the GPU, quantized there (bit-exact quantizer) and
     replicated into enough copies to rotate a >= 2 GiB working set, so the
     MALL cannot serve the stream;
