@@ -12,7 +12,12 @@ arithmetic:
 * paged cache: position j of sequence b is row j % page_rows of page
   block_table[b][j // page_rows], each page holding [Hkv][page_rows][...]
   (:func:`scatter_rows` writes a contiguous cache into pages,
-  :func:`gather_rows` reads it back).
+  :func:`gather_rows` reads it back);
+* the magnitude of each output, sum_j p_j |v_jd| with the same softmax
+  weights (:func:`magnitude_gqa`): the scale of the summands an fp32 kernel
+  accumulates, which sets its rounding error where the output itself cancels
+  far below it. Not part of the reference; the randomized tests use it to
+  size their error bound.
 
 Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline import this
 package; the product never does.
@@ -37,6 +42,27 @@ def reference_gqa(kd: np.ndarray, vd: np.ndarray, q: np.ndarray, Hq: int, Hkv: i
     vr = np.repeat(np.asarray(vd, np.float32).reshape(Hkv, L, D), g, axis=0)
     return _reference(np.ascontiguousarray(kr).ravel(), np.ascontiguousarray(vr).ravel(),
                       np.ascontiguousarray(q).ravel(), Hq, L, D, threads=threads)
+
+
+def magnitude_gqa(kd: np.ndarray, vd: np.ndarray, q: np.ndarray, Hq: int, Hkv: int, L: int,
+                  D: int) -> np.ndarray:
+    """sum_j p_hj |v_jd| in double, p_h the softmax of q_h . k_j / sqrt(D) over the
+    KV head of query head h (the weights of reference(), src/voltattn.cu:776-791).
+
+    kd, vd: float32 [Hkv][L][D]; q: fp16 bits [Hq][D]. Returns float64 [Hq*D].
+    It equals |reference| when every v_jd >= 0 and bounds it from above."""
+    if Hq % Hkv:
+        raise ValueError("Hq must be a multiple of Hkv")
+    g = Hq // Hkv
+    k = np.asarray(kd, np.float32).reshape(Hkv, L, D).astype(np.float64)
+    v = np.abs(np.asarray(vd, np.float32).reshape(Hkv, L, D).astype(np.float64))
+    qf = np.asarray(q).view(np.float16).reshape(Hq, D).astype(np.float64)
+    out = np.empty((Hq, D), np.float64)
+    for h in range(Hq):
+        s = k[h // g] @ qf[h] / np.sqrt(D)
+        p = np.exp(s - s.max())
+        out[h] = (p @ v[h // g]) / p.sum()
+    return out.ravel()
 
 
 def scatter_rows(pool: np.ndarray, rows: np.ndarray, table: np.ndarray, page_rows: int) -> None:

@@ -66,6 +66,7 @@ class PagedBatch:
             self.vspool = rng.integers(0, 65536, (num_pages, Hkv, page_rows, D // G), dtype=np.uint16)
         self.q = queries(B * Hq, D, seed + 1).reshape(B, Hq, D)
         self.ref = np.zeros((B, Hq, D), np.float32)
+        self.mag = np.zeros((B, Hq, D), np.float64)     # sum_j p_j |v_jd| (error scale of cancelling outputs)
         for b, L in enumerate(self.lens):
             if L == 0:
                 continue
@@ -76,6 +77,7 @@ class PagedBatch:
                 batch.scatter_rows(self.kspool, c["ksc"], self.table[b], page_rows)
                 batch.scatter_rows(self.vspool, c["vsc"], self.table[b], page_rows)
             self.ref[b] = batch.reference_gqa(c["kd"], c["vd"], self.q[b], Hq, Hkv, L, D).reshape(Hq, D)
+            self.mag[b] = batch.magnitude_gqa(c["kd"], c["vd"], self.q[b], Hq, Hkv, L, D).reshape(Hq, D)
         self.shape = va.PagedShape(B, Hq, Hkv, D, G, page_rows, self.max_pages, num_pages,
                                    max_seq_len if max_seq_len is not None else max(max(self.lens), 1))
         self.seq_lens = np.asarray(self.lens, np.int32)

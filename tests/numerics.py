@@ -14,3 +14,13 @@ def tight_bound(ref) -> np.ndarray:
     half an fp16 ulp plus 2e-6 relative fp32 accumulation error."""
     r = np.asarray(ref, np.float64)
     return half_ulp(r) + 2e-6 * np.abs(r) + 1e-7
+
+
+def cond_bound(ref, mag) -> np.ndarray:
+    """tight_bound widened by the rounding of the fp32 arithmetic itself where an
+    output cancels: the terms a kernel accumulates have magnitude
+    mag = sum_j p_j |v_jd| (oracle.batch.magnitude_gqa), and scores, weights and
+    sums are each rounded at that scale, so |error| may reach a few fp32 ulps of
+    mag even when |ref| is 1000x smaller. Adds 8 fp32 ulps (2^-21) of mag; for
+    an output that does not cancel (mag ~ |ref|) that is under 5e-7 |ref|."""
+    return tight_bound(ref) + 2.0 ** -21 * np.asarray(mag, np.float64)

@@ -2,7 +2,11 @@
 cases, these draw the shape itself. Every draw is deterministic (fixed seed per
 case id), printed before it runs, and checked against the oracle's double
 reference with the reference's gate (src/voltattn.cu:903) and the fp16
-rounding bound (tests/numerics.py).
+rounding bound widened by 8 fp32 ulps of each output's magnitude
+sum_j p_j |v_jd| (tests/numerics.py cond_bound): random draws include outputs
+that cancel 1000x below the terms summed into them (an extended sweep met one,
+q4+ at L = 16, just over the plain bound), where any fp32 kernel's rounding is
+set by that magnitude, not by |ref|.
 
 * decode: any of the seven formats, H 1-24, L 1-6000 (log-uniform), D 64/128,
   G 32/64, S 1-64 (more splits take the separate merge pass, which the paged
@@ -18,7 +22,7 @@ import oracle
 from oracle import batch
 import voltattn_amd as va
 from tests import batch_util, gpu_util
-from tests.numerics import tight_bound
+from tests.numerics import cond_bound
 
 pytestmark = pytest.mark.gpu
 
@@ -26,13 +30,13 @@ ALL = [va.Fmt.F16, va.Fmt.F16M, va.Fmt.Q8, va.Fmt.Q8M, va.Fmt.Q4, va.Fmt.Q4M, va
 TILED = [va.Fmt.F16M, va.Fmt.Q8M, va.Fmt.Q4M, va.Fmt.Q3M]
 
 
-def _check(got, ref, what):
+def _check(got, ref, what, mag):
     got = np.asarray(got, np.float32).ravel()
     ref = np.asarray(ref, np.float64).ravel()
     assert np.all(np.isfinite(got)), what
     ok, maxerr = oracle.gate(got, ref)
     assert ok, (what, maxerr)
-    bound = tight_bound(ref)
+    bound = cond_bound(ref, np.asarray(mag, np.float64).ravel())
     assert np.all(np.abs(got - ref) <= bound), (what, float(np.max(np.abs(got - ref) / bound)))
 
 
@@ -53,7 +57,7 @@ def test_fuzz_decode(case):
     print("case", case, what, flush=True)
     c = gpu_util.case(va.fmt_bits(fmt), H, L, D, G, 0xA000 + case)
     got = gpu_util.run_case(fmt, c, S)["out"]
-    _check(got, c["ref"], what)
+    _check(got, c["ref"], what, batch.magnitude_gqa(c["kd"], c["vd"], c["q"], H, H, L, D))
 
 
 @pytest.mark.parametrize("case", range(48))
@@ -87,7 +91,8 @@ def test_fuzz_gqa(case):
     finally:
         for x in bufs:
             x.free()
-    _check(got, batch.reference_gqa(c["kd"], c["vd"], q, Hq, Hkv, L, D), what)
+    _check(got, batch.reference_gqa(c["kd"], c["vd"], q, Hq, Hkv, L, D), what,
+           batch.magnitude_gqa(c["kd"], c["vd"], q, Hq, Hkv, L, D))
 
 
 @pytest.mark.parametrize("case", range(32))
@@ -108,4 +113,4 @@ def test_fuzz_paged(case):
         got = pb.run()
     finally:
         pb.free()
-    _check(got, pb.ref, what)
+    _check(got, pb.ref, what, pb.mag)

@@ -88,3 +88,35 @@ def test_paged_round_trip_random():
         rows = rng.integers(0, 255, (Hkv, L, W), dtype=np.uint8)
         batch.scatter_rows(pool, rows, table, P)
         np.testing.assert_array_equal(batch.gather_rows(pool, table, L, P), rows)
+
+
+def _draw(Hkv, L, D, seed, positive=False):
+    rng = np.random.default_rng(seed)
+    kd = rng.standard_normal((Hkv, L, D)).astype(np.float32)
+    vd = rng.standard_normal((Hkv, L, D)).astype(np.float32)
+    if positive:
+        vd = np.abs(vd) + np.arange(Hkv, dtype=np.float32)[:, None, None]   # heads differ by offset
+    return kd, vd
+
+
+@pytest.mark.parametrize("Hq,Hkv,L,D", [(4, 2, 37, 64), (6, 3, 300, 128), (2, 2, 5, 128)])
+def test_magnitude_is_the_reference_for_nonnegative_v(Hq, Hkv, L, D):
+    # sum_j p_j |v_jd| = sum_j p_j v_jd when V >= 0: the same weights and head mapping as reference()
+    kd, vd = _draw(Hkv, L, D, 0xA11 + L, positive=True)
+    q = _f16(np.random.default_rng(L).standard_normal((Hq, D)))
+    mag = batch.magnitude_gqa(kd, vd, q, Hq, Hkv, L, D)
+    ref = batch.reference_gqa(kd, vd, q, Hq, Hkv, L, D).astype(np.float64)
+    np.testing.assert_allclose(mag, ref, rtol=2e-6)
+
+
+def test_magnitude_bounds_the_reference_and_closed_forms():
+    Hq, Hkv, L, D = 6, 2, 200, 64
+    kd, vd = _draw(Hkv, L, D, 0xA12)
+    q = _f16(np.random.default_rng(7).standard_normal((Hq, D)))
+    mag = batch.magnitude_gqa(kd, vd, q, Hq, Hkv, L, D)
+    ref = batch.reference_gqa(kd, vd, q, Hq, Hkv, L, D).astype(np.float64)
+    assert np.all(mag >= np.abs(ref) - 1e-6 * mag)
+    assert np.mean(mag > 2 * np.abs(ref)) > 0.2            # signed V cancels: the bound is not |ref|
+    # one position: the weight is 1, so the magnitude is |v_0| exactly
+    mag1 = batch.magnitude_gqa(kd[:, :1], vd[:, :1], q, Hq, Hkv, 1, D).reshape(Hq, D)
+    np.testing.assert_array_equal(mag1, np.abs(np.repeat(vd[:, 0], Hq // Hkv, axis=0)).astype(np.float64))
