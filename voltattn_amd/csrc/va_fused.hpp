@@ -103,8 +103,9 @@ struct Route {
 // words; a word whose tag is stale belongs to a group that has already arrived
 // and issued its stores, so it is re-read (bounded) until it lands.
 //
-// The merge spreads the loads over all NT/64 waves (coherent loads are
-// serviced one instruction at a time) and runs the query slots side by side:
+// The merge spreads the loads over all NT/64 waves (a wave's coherent loads
+// are serviced one instruction at a time; one wave doing all of them measured
+// 0.5-0.9 us slower) and runs the query slots side by side:
 // WQ = NW/QG waves per slot; lane j of each of them reads split j's (m, l),
 // and sub-wave sw folds splits j = sw, sw + WQ, ... in increasing order into
 // lane-pair columns (2i, 2i+1) with split j's weight read by readlane; the WQ
