@@ -157,6 +157,14 @@ const char* va_fmt_name(va_fmt fmt);
 int va_quantize(int bits, int G, const float* x, size_t rows, int D, void* packed,
                 uint16_t* scales, void* stream);
 
+/* Device-side inverse of va_quantize: packed codes (rows*D*bits/8 bytes,
+ * 4-byte aligned) and fp16 scales (rows*(D/G)) to fp32 values out[rows][D]
+ * (16-byte aligned), bit-exact with the reference's host dq()
+ * (src/voltattn.cu:747-767): float(scale) * code, exact in fp32. bits in
+ * {8,4,3}, G in {32,64}. */
+int va_dequantize(int bits, int G, const void* packed, const uint16_t* scales, size_t rows, int D,
+                  float* out, void* stream);
+
 /* Device-side fp32 -> fp16 round-to-nearest-even over n values (the
  * reference's __float2half loops, src/voltattn.cu:866-868, 1000-1002). */
 int va_f32_to_f16(const float* x, size_t n, uint16_t* out, void* stream);

@@ -125,6 +125,15 @@ def test_quantize_and_merge_argument_checks():
     assert va.lib.va_quantize(8, 48, 0x1000, 10, 128, 0x2000, 0x3000, None) == VA_EINVAL
     assert va.lib.va_quantize(8, 32, None, 10, 128, 0x2000, 0x3000, None) == VA_ENULL
     assert va.lib.va_quantize(8, 32, 0x1004, 10, 128, 0x2000, 0x3000, None) == VA_EALIGN
+    # va_dequantize: same rules, out 16-byte aligned; rows = 0 is a no-op (no device access)
+    assert va.lib.va_dequantize(5, 32, 0x1000, 0x2000, 10, 128, 0x3000, None) == VA_EINVAL
+    assert va.lib.va_dequantize(8, 64, 0x1000, 0x2000, 10, 96, 0x3000, None) == VA_EINVAL
+    assert va.lib.va_dequantize(4, 32, None, 0x2000, 10, 128, 0x3000, None) == VA_ENULL
+    assert va.lib.va_dequantize(4, 32, 0x1000, 0x2000, 10, 128, None, None) == VA_ENULL
+    assert va.lib.va_dequantize(3, 32, 0x1002, 0x2000, 10, 128, 0x3000, None) == VA_EALIGN
+    assert va.lib.va_dequantize(3, 32, 0x1000, 0x2001, 10, 128, 0x3000, None) == VA_EALIGN
+    assert va.lib.va_dequantize(3, 32, 0x1000, 0x2000, 10, 128, 0x3008, None) == VA_EALIGN
+    assert va.lib.va_dequantize(3, 32, 0x1000, 0x2000, 0, 128, 0x3000, None) == VA_OK
     assert va.lib.va_merge(None, 0x1000, 4, 128, 2, None) == VA_ENULL
     assert va.lib.va_merge(0x1000, 0x2000, 4, 96, 2, None) == VA_EINVAL
 

@@ -3,7 +3,8 @@ PyTorch fp32 reference: softmax(q.K^T / sqrt(D)).V over the K/V values the
 oracle's dequant gives for the packed bytes (dq(), src/voltattn.cu:747-767).
 Tolerance: the tight bound of tests/numerics.py (half an fp16 ulp + 2e-6|ref|)
 plus 2e-6 absolute for the fp32 reference's own rounding. quantize and
-append_kv are checked bit for bit against the oracle's quantizer."""
+append_kv are checked bit for bit against the oracle's quantizer, dequantize
+against the oracle's dq()."""
 import numpy as np
 import pytest
 import torch
@@ -115,3 +116,14 @@ def test_quantize_op_is_bit_exact(bits):
     data, sc = oracle.quantize(x.numpy().ravel(), 128, 32, bits)
     np.testing.assert_array_equal(packed.cpu().numpy().ravel(), data)
     np.testing.assert_array_equal(scales.cpu().numpy().view(np.uint16).ravel(), sc)
+
+
+@pytest.mark.parametrize("bits,G", [(8, 32), (4, 64), (3, 32)])
+def test_dequantize_op_is_bit_exact(bits, G):
+    x = torch.randn(3, 50, 128, generator=torch.Generator().manual_seed(10 + bits))
+    packed, scales = torch.ops.voltattn.quantize(x.to(DEV), bits, G)
+    out = torch.ops.voltattn.dequantize(packed, scales, bits, G)
+    assert out.shape == (3, 50, 128) and out.dtype == torch.float32
+    want = oracle.dequant(packed.cpu().numpy().ravel(), scales.cpu().numpy().view(np.uint16).ravel(),
+                          150, 128, G, bits)
+    np.testing.assert_array_equal(out.cpu().numpy().ravel().view(np.uint32), want.view(np.uint32))

@@ -9,7 +9,7 @@ import voltattn_amd.torch_ops  # noqa: F401  (registers torch.ops.voltattn.*)
 
 
 def test_ops_registered():
-    for name in ("decode", "decode_gqa", "decode_paged", "append_kv", "quantize"):
+    for name in ("decode", "decode_gqa", "decode_paged", "append_kv", "quantize", "dequantize"):
         assert hasattr(torch.ops.voltattn, name), name
 
 
@@ -31,6 +31,11 @@ def test_fake_shapes_on_meta():
     assert out.shape == (4, 32, 128) and out.dtype == torch.float16
     packed, scales = torch.ops.voltattn.quantize(torch.empty(10, 128, **m), 3, 32)
     assert packed.shape == (10, 48) and scales.shape == (10, 4)
+    x = torch.ops.voltattn.dequantize(packed, scales, 3, 32)
+    assert x.shape == (10, 128) and x.dtype == torch.float32
+    x = torch.ops.voltattn.dequantize(torch.empty(2, 5, 32, dtype=torch.uint8, **m),
+                                      torch.empty(2, 5, 1, dtype=torch.float16, **m), 4, 64)
+    assert x.shape == (2, 5, 64)
 
 
 def test_cpu_tensors_refused():
@@ -41,6 +46,9 @@ def test_cpu_tensors_refused():
         torch.ops.voltattn.decode(q, k, k, s, s, "q8+")
     with pytest.raises(RuntimeError, match="gfx950"):
         torch.ops.voltattn.quantize(torch.zeros(2, 128), 8, 32)
+    with pytest.raises(RuntimeError, match="gfx950"):
+        torch.ops.voltattn.dequantize(torch.zeros(2, 128, dtype=torch.uint8),
+                                      torch.zeros(2, 4, dtype=torch.float16), 8, 32)
 
 
 M = dict(device="meta")
@@ -135,3 +143,19 @@ def test_quantize_rejects_bad_arguments():
         torch.ops.voltattn.quantize(_t(4, 128, dtype=torch.float16), 8, 32)
     with pytest.raises(RuntimeError, match="group must be"):
         torch.ops.voltattn.quantize(_t(4, 96, dtype=torch.float32), 8, 64)
+
+
+def test_dequantize_rejects_bad_arguments():
+    sc = _t(4, 4, dtype=torch.float16)
+    with pytest.raises(RuntimeError, match="bits must be"):
+        torch.ops.voltattn.dequantize(_t(4, 128), sc, 5, 32)
+    with pytest.raises(RuntimeError, match="packed must be uint8"):
+        torch.ops.voltattn.dequantize(_t(4, 128, dtype=torch.float16), sc, 8, 32)
+    with pytest.raises(RuntimeError, match="whole 3-bit codes"):
+        torch.ops.voltattn.dequantize(_t(4, 47), sc, 3, 32)
+    with pytest.raises(RuntimeError, match="group must be"):
+        torch.ops.voltattn.dequantize(_t(4, 48), sc, 4, 64)          # D = 96
+    with pytest.raises(RuntimeError, match="scales has shape"):
+        torch.ops.voltattn.dequantize(_t(4, 64), _t(4, 2, dtype=torch.float16), 4, 32)
+    with pytest.raises(RuntimeError, match="scales has dtype"):
+        torch.ops.voltattn.dequantize(_t(4, 64), _t(4, 4, dtype=torch.float32), 4, 32)

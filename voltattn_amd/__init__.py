@@ -25,7 +25,7 @@ import numpy as np
 
 __all__ = [
     "Fmt", "DeviceBufs", "VAError", "launch", "decode_splits", "merge", "ws_bytes",
-    "payload_bytes", "scale_bytes", "split_chunk", "pick_splits", "quantize", "f32_to_f16",
+    "payload_bytes", "scale_bytes", "split_chunk", "pick_splits", "quantize", "dequantize", "f32_to_f16",
     "fill_normal", "probe_read", "merge_faults", "device_info", "device_count", "DeviceBuffer", "Event",
     "Stream", "Graph", "sync", "lib", "LIB_PATH", "fmt_bits", "is_f16", "check",
     "PagedShape", "PagedBufs", "decode_gqa", "pick_splits_gqa", "decode_paged",
@@ -103,6 +103,7 @@ _sig("va_split_chunk", _I, _I, _I)
 _sig("va_pick_splits", _I, _I, _I, _I, _I, C.POINTER(_I))
 _sig("va_fmt_name", C.c_char_p, _I)
 _sig("va_quantize", _I, _I, _I, _P, _SZ, _I, _P, _P, _P)
+_sig("va_dequantize", _I, _I, _I, _P, _P, _SZ, _I, _P, _P)
 _sig("va_f32_to_f16", _I, _P, _SZ, _P, _P)
 _sig("va_fill_normal", _I, _P, _SZ, _U64, _P)
 _sig("va_probe_read", _I, _SZ, _I, C.POINTER(C.c_double))
@@ -339,6 +340,11 @@ def pick_splits(f: Fmt, H: int, L: int, D: int) -> int:
 
 def quantize(bits: int, G: int, x: int, rows: int, D: int, packed: int, scales: int, stream=None) -> None:
     check(lib.va_quantize(bits, G, x, rows, D, packed, scales, _stream(stream)))
+
+
+def dequantize(bits: int, G: int, packed: int, scales: int, rows: int, D: int, out: int, stream=None) -> None:
+    """va_dequantize: packed codes + fp16 scales (device pointers) to fp32 out[rows][D]."""
+    check(lib.va_dequantize(bits, G, packed, scales, rows, D, out, _stream(stream)))
 
 
 def f32_to_f16(x: int, n: int, out: int, stream=None) -> None:

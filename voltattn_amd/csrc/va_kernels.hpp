@@ -118,6 +118,11 @@ hipError_t launch_empty(int grid, float* sink, hipStream_t stream);
 hipError_t launch_quantize(int bits, int G, const float* x, size_t rows, int D,
                            uint8_t* packed, uint16_t* scales, hipStream_t stream);
 
+// Inverse of the quantizer: packed codes + fp16 scales of rows x D elements to
+// fp32 (bits 8/4/3, G 32/64), bit-exact with the reference's dq().
+hipError_t launch_dequantize(int bits, int G, const uint8_t* packed, const uint16_t* scales, size_t rows,
+                             int D, float* out, hipStream_t stream);
+
 // Quantize-and-append of n new fp16 rows per (sequence, KV head) into a page
 // pool [num_pages][hkv][page_rows][row bytes] (+ fp16 scales [...][D/G]).
 struct AppendArgs {

@@ -6,6 +6,8 @@
 //     G in {32, 64}: amax in fp32, s = amax/lim (IEEE division), the fp16
 //     scale rounded to nearest even, codes clamp(rint(x / float(scale))), with
 //     a non-finite quotient giving code 0 as x86-64 lrint + int truncation does;
+//   * dequantize_groups: the inverse, packed codes and fp16 scales back to
+//     fp32 values, bit-exact with the reference's dq() (src/voltattn.cu:747-767);
 //   * f32_to_f16: round-to-nearest-even conversion of fp32 arrays (the
 //     reference's __float2half over the f16-format K/V, src/voltattn.cu:866-868);
 //   * fill_normal: seeded N(0,1) bench data, Philox4x32-10 (Salmon et al.,
@@ -90,6 +92,45 @@ __global__ __launch_bounds__(256) void quantize_groups(const float* __restrict__
             xv[4 * c] = w.x; xv[4 * c + 1] = w.y; xv[4 * c + 2] = w.z; xv[4 * c + 3] = w.w;
         }
         quant_group<BITS, G>(xv, packed + gi * (G * BITS / 8), scales + gi);
+    }
+}
+
+// Inverse of the packer, one thread per group: value = float(scale) * code.
+// The reference's dq() forms the same product in double; an fp16 scale times a
+// code of at most 7 bits is exact in fp32 (non-finite scales give the same
+// inf/NaN), so the results are equal bit for bit. Code layouts as in
+// quant_group: q8 int8, q4 nibble + 8 (low nibble first), q3 3-bit fields + 4.
+template <int BITS, int G>
+__global__ __launch_bounds__(256) void dequantize_groups(const uint8_t* __restrict__ packed,
+                                                         const uint16_t* __restrict__ scales,
+                                                         size_t ngroups, float* __restrict__ out) {
+    constexpr int NW = G * BITS / 32;              // packed words per group
+    const size_t stride = (size_t)gridDim.x * blockDim.x;
+    for (size_t gi = (size_t)blockIdx.x * blockDim.x + threadIdx.x; gi < ngroups; gi += stride) {
+        const uint32_t* src = reinterpret_cast<const uint32_t*>(packed + gi * (G * BITS / 8));
+        uint32_t w[NW];
+#pragma unroll
+        for (int k = 0; k < NW; ++k) w[k] = src[k];
+        const float s = h2f(scales[gi]);
+        float v[G];
+#pragma unroll
+        for (int i = 0; i < G; ++i) {
+            int c;
+            if constexpr (BITS == 8) {
+                c = (int)(int8_t)(uint8_t)(w[i / 4] >> (8 * (i % 4)));
+            } else if constexpr (BITS == 4) {
+                c = (int)((w[i / 8] >> (4 * (i % 8))) & 15u) - 8;
+            } else {
+                const int b = 3 * i;
+                uint32_t f = w[b / 32] >> (b % 32);
+                if (b % 32 > 29) f |= w[b / 32 + 1] << (32 - b % 32);
+                c = (int)(f & 7u) - 4;
+            }
+            v[i] = s * (float)c;
+        }
+        f32x4* dst = reinterpret_cast<f32x4*>(out + gi * G);
+#pragma unroll
+        for (int k = 0; k < G / 4; ++k) dst[k] = f32x4{v[4 * k], v[4 * k + 1], v[4 * k + 2], v[4 * k + 3]};
     }
 }
 
@@ -216,6 +257,20 @@ hipError_t launch_quantize(int bits, int G, const float* x, size_t rows, int D, 
         if (bits == 8) VA_QLAUNCH(8, 64); else if (bits == 4) VA_QLAUNCH(4, 64); else VA_QLAUNCH(3, 64);
     }
 #undef VA_QLAUNCH
+    return hipGetLastError();
+}
+
+hipError_t launch_dequantize(int bits, int G, const uint8_t* packed, const uint16_t* scales, size_t rows,
+                             int D, float* out, hipStream_t stream) {
+    const size_t ngroups = rows * (size_t)(D / G);
+    const dim3 grid(grid_for(ngroups)), block(256);
+#define VA_DLAUNCH(B, GG) hipLaunchKernelGGL((dequantize_groups<B, GG>), grid, block, 0, stream, packed, scales, ngroups, out)
+    if (G == 32) {
+        if (bits == 8) VA_DLAUNCH(8, 32); else if (bits == 4) VA_DLAUNCH(4, 32); else VA_DLAUNCH(3, 32);
+    } else {
+        if (bits == 8) VA_DLAUNCH(8, 64); else if (bits == 4) VA_DLAUNCH(4, 64); else VA_DLAUNCH(3, 64);
+    }
+#undef VA_DLAUNCH
     return hipGetLastError();
 }
 

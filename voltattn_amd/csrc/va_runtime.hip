@@ -588,6 +588,21 @@ int va_quantize(int bits, int G, const float* x, size_t rows, int D, void* packe
     return VA_OK;
 }
 
+int va_dequantize(int bits, int G, const void* packed, const uint16_t* scales, size_t rows, int D,
+                  float* out, void* stream) {
+    if (!(bits == 8 || bits == 4 || bits == 3)) return fail(VA_EINVAL, "bits must be 8, 4 or 3");
+    if (!((G == 32 || G == 64) && D >= G && D % G == 0 && D % 8 == 0))
+        return fail(VA_EINVAL, "G must be 32 or 64 and divide D");
+    if (!packed || !scales || !out) return fail(VA_ENULL, "packed, scales and out must be non-NULL");
+    if (!aligned(packed, 4) || !aligned(scales, 2) || !aligned(out, 16))
+        return fail(VA_EALIGN, "packed needs 4-byte, scales 2-byte, out 16-byte alignment");
+    if (rows == 0) return VA_OK;
+    const hipError_t e = va::launch_dequantize(bits, G, static_cast<const uint8_t*>(packed), scales, rows, D,
+                                               out, as_stream(stream));
+    if (e != hipSuccess) return hip_fail(e, "dequantize launch");
+    return VA_OK;
+}
+
 int va_f32_to_f16(const float* x, size_t n, uint16_t* out, void* stream) {
     if (!x || !out) return fail(VA_ENULL, "x and out must be non-NULL");
     if (n == 0) return VA_OK;

@@ -8,6 +8,7 @@
 //                         (src/voltattn.cu:813-833 and combine, 651-672)
 //   voltattn::pick_splits the reference's split rule (src/voltattn.cu:1026)
 //   voltattn::quantize    device quantize() (src/voltattn.cu:705-745)
+//   voltattn::dequantize  device dq() over whole rows (src/voltattn.cu:747-767)
 //
 // Beyond the reference (its README.md:205-206 lists GQA and paged KV as
 // missing): launch_gqa, launch_paged, append_kv, and the Stream / Graph
@@ -163,6 +164,12 @@ inline void append_kv(Fmt f, const uint16_t* x, int n, const int32_t* start, con
 inline void quantize(int bits, int G, const float* x, size_t rows, int D, void* packed, uint16_t* scales,
                      void* stream = nullptr) {
     check(va_quantize(bits, G, x, rows, D, packed, scales, stream));
+}
+
+// Device dq() of packed codes + fp16 scales back to fp32 rows [rows][D].
+inline void dequantize(int bits, int G, const void* packed, const uint16_t* scales, size_t rows, int D,
+                       float* out, void* stream = nullptr) {
+    check(va_dequantize(bits, G, packed, scales, rows, D, out, stream));
 }
 
 // RAII device allocation.

@@ -8,7 +8,9 @@ Importing this module registers
 * ``voltattn::decode_paged(...)`` — a batch over a page pool (va_decode_paged);
 * ``voltattn::append_kv(...)`` — quantize-and-append new rows (va_append_kv; mutates the pools);
 * ``voltattn::quantize(x, bits, group) -> (packed, scales)`` (va_quantize; the reference's
-  quantize(), src/voltattn.cu:705-745).
+  quantize(), src/voltattn.cu:705-745);
+* ``voltattn::dequantize(packed, scales, bits, group) -> x`` (va_dequantize; the reference's
+  dq(), src/voltattn.cu:747-767, over whole rows: fp32 [..., D]).
 
 Tensors keep the C ABI's layouts (include/voltattn.h): q/out fp16 [.., H, D];
 quantized K/V payload uint8 [.., L, row bytes]; f16 K/V fp16 [.., L, D]; scales
@@ -29,7 +31,7 @@ import torch
 
 from . import (Fmt, _Bufs, _PagedBufs, _PagedShape, check, fmt_bits, lib, row_bytes, ws_bytes)
 
-__all__ = ["decode", "decode_gqa", "decode_paged", "append_kv", "quantize"]
+__all__ = ["decode", "decode_gqa", "decode_paged", "append_kv", "quantize", "dequantize"]
 
 
 def _fmt(name: str) -> Fmt:
@@ -158,6 +160,22 @@ def _validate_quantize(x, bits: int, group: int) -> None:
     D = int(x.shape[-1]) if x.dim() else 0
     if not (group in (32, 64) and D >= group and D % group == 0 and D % 8 == 0):
         _fail(f"group must be 32 or 64 and divide D (got group={group}, D={D})")
+
+
+def _validate_dequantize(packed, scales, bits: int, group: int) -> int:
+    """Checks packed uint8 [..., D*bits/8] and scales fp16 [..., D/G]; returns D."""
+    if bits not in (8, 4, 3):
+        _fail(f"bits must be 8, 4 or 3 (got {bits})")
+    if packed.dtype != torch.uint8:
+        _fail(f"packed must be uint8 (got {packed.dtype})")
+    nb = int(packed.shape[-1]) if packed.dim() else 0
+    if nb * 8 % bits:
+        _fail(f"packed rows of {nb} bytes do not hold whole {bits}-bit codes")
+    D = nb * 8 // bits
+    if not (group in (32, 64) and D >= group and D % group == 0 and D % 8 == 0):
+        _fail(f"group must be 32 or 64 and divide D (got group={group}, D={D})")
+    _expect(scales, "scales", tuple(packed.shape[:-1]) + (D // group,), torch.float16)
+    return D
 
 
 @torch.library.custom_op("voltattn::decode", mutates_args=())
@@ -291,6 +309,23 @@ def _(x, bits, group=32):
     D = x.shape[-1]
     return (x.new_empty(x.shape[:-1] + (D * bits // 8,), dtype=torch.uint8),
             x.new_empty(x.shape[:-1] + (D // group,), dtype=torch.float16))
+
+
+@torch.library.custom_op("voltattn::dequantize", mutates_args=())
+def dequantize(packed: torch.Tensor, scales: torch.Tensor, bits: int, group: int = 32) -> torch.Tensor:
+    """(packed uint8 [..., D*bits/8], fp16 scales [..., D/G]) -> fp32 [..., D], bit-exact dq()."""
+    D = _validate_dequantize(packed, scales, bits, group)
+    _need_gpu(packed, scales)
+    rows = packed.numel() // max(1, int(packed.shape[-1]))
+    out = torch.empty(packed.shape[:-1] + (D,), dtype=torch.float32, device=packed.device)
+    check(lib.va_dequantize(bits, group, _ptr(packed), _ptr(scales), rows, D, _ptr(out), _stream(packed)))
+    return out
+
+
+@dequantize.register_fake
+def _(packed, scales, bits, group=32):
+    D = _validate_dequantize(packed, scales, bits, group)
+    return packed.new_empty(packed.shape[:-1] + (D,), dtype=torch.float32)
 
 
 def row_format_bits(fmt: str) -> int:
