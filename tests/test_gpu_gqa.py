@@ -79,6 +79,26 @@ def test_gqa_d64_g64(fmt):
     _check(got, ref, fmt.label)
 
 
+@pytest.mark.parametrize("fmt", TILED, ids=lambda f: f.label)
+def test_gqa_d128_g64(fmt):
+    # two scale groups per row: the matrix-core forms stack NG = 2 columns per query slot
+    print(f"gqa d128 g64 {fmt.label}", flush=True)
+    got, ref = _run(fmt, 12, 3, 1500, 128, 64, 0, 0x12864)
+    _check(got, ref, fmt.label)
+
+
+@pytest.mark.parametrize("fmt", TILED, ids=lambda f: f.label)
+def test_paged_d128_g64(fmt):
+    print(f"paged d128 g64 {fmt.label}", flush=True)
+    pb = batch_util.PagedBatch(fmt, [700, 1, 1300], 8, 2, 128, 64, 256, seed=0x6464)
+    try:
+        got = pb.run()
+    finally:
+        pb.free()
+    for b in range(3):
+        _check(got[b].astype(np.float32).ravel(), pb.ref[b].ravel(), (fmt.label, "paged", b))
+
+
 def test_gqa_single_position():
     got, ref = _run(va.Fmt.Q8M, 8, 2, 1, 128, 32, 0, 0x1)
     _check(got, ref, "L=1")
