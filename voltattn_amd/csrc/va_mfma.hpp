@@ -532,8 +532,11 @@ __global__ __launch_bounds__(WAVES * 64, 1) void decode_mfma(DecodeArgs a) {
         // dispatcher's round-robin placement) busy on the vector ALU, and the
         // older one wins issue: it runs ahead, and the other finishes alone with
         // half the loads in flight. Each wave posts its tile pair in LDS and
-        // takes issue priority while it trails its partner (a stale entry left
-        // by an earlier group changes one pair's priority, nothing else).
+        // takes issue priority while it trails its partner. The entries are
+        // not cleared first: the partner's entry may still hold what an earlier
+        // work-group on this CU left there, which only sets one pair's
+        // priority, never a result (clearing both entries before the loop
+        // measured ~1 us slower for grouped q4+ and q3+ at L 65536).
         // Measured on MI355X, Hq 32 / Hkv 8, 7 interleaved rounds: L 65536 q4+
         // 24.5 -> 24.3 us, q3+ 28.6 -> 28.3 us; paged B 8 x 16384 q4+ 45.6 ->
         // 43.5 us. q8 rows lose ~0.2 us with it and keep free issue.
