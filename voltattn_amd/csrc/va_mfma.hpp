@@ -6,21 +6,28 @@
 // heads; here the matrix core does the multiply-adds and the VALU keeps the
 // unpack, the softmax and the operand set-up).
 //
-// MFMA 16x16x32 f16 lane layout (probed on MI355X): lane l holds
-// A[l%16][8(l/16)+e] and B[8(l/16)+e][l%16] (e = 0..7) and receives
-// D[4(l/16)+v][l%16] (v = 0..3). Below, quarter g = l/16 and column n = l%16.
+// MFMA lane layouts (probed on MI355X): for 16x16x32 f16, lane l holds
+// A[l%16][8(l/16)+e] and B[8(l/16)+e][l%16] (e = 0..7); for 16x16x64 i8,
+// A[l%16][16(l/16)+e] and B[16(l/16)+e][l%16] (e = 0..15, byte order); both
+// return D[4(l/16)+v][l%16] (v = 0..3). Below, quarter g = l/16 and column
+// n = l%16.
 //
-// q.K — one 16-row block of positions per MFMA row index, k = dimensions.
-//   A = K codes of 16 rows: lane (g, n) loads the D/4 contiguous bytes
-//       [g*D/4, (g+1)*D/4) of row n and turns them into exact fp16 integers.
-//   B = q^T with the scale groups stacked as columns: column n = cg*QP + cq
-//       (QP = 16/NG column slots per group) holds query slot cq restricted to
-//       the dimensions of scale group cg (zero elsewhere). Every product
-//       code*q is exact in fp32, so each output column is the exact partial
-//       dot of one (query, group); the per-position group scales are applied
-//       afterwards in fp32 and the NG columns of a query are summed with DPP
-//       row rotations (every replica gets the same bits).
-// P.V — k = positions, 32 per MFMA (the two q.K blocks).
+// q.K — two 16-row blocks of positions per 32-row wave tile, k = dimensions,
+// on v_mfma_i32_16x16x64_i8 (exact integer products and sums).
+//   A = the K codes of 16 rows as unsigned or signed bytes: q8's int8 codes as
+//       loaded, q4's nibbles and q3's 3-bit fields spread to bytes n = v + 8 /
+//       v + 4 (the offset's -8 or -4 times the column sum of q is the int32
+//       accumulator's start value).
+//   B = q as three balanced int8 digits of round(q * 2^sh) (sh per column puts
+//       max |q| in [2^21, 2^22)), with the scale groups stacked as columns:
+//       column n = cg*QP + cq (QP = 16/NG column slots per group) holds query
+//       slot cq restricted to the dimensions of scale group cg (zero
+//       elsewhere). Each digit's dot with the codes is exact in int32; the
+//       three are recombined in fp32 with one rounding, so each output column
+//       is the partial dot of one (query, group); the per-position group scales
+//       are applied afterwards in fp32 and the NG columns of a query are summed
+//       with DPP row rotations (every replica gets the same bits).
+// P.V — k = positions, 32 per f16 MFMA (the two q.K blocks).
 //   A = P * s_v with the same stacked rows: row n = (cg, cq) carries
 //       p[cq][pos] * s_v[pos][cg]. Lane (g, n) already holds the scores of
 //       exactly the positions of its k slots (16c + 4g + v), so no data moves.
