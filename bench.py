@@ -36,6 +36,11 @@ Method (reference bench, src/voltattn.cu:967-1070, re-derived for MI355X):
     payload + fp16 scales: 2*H*L*(D*b/8 + 2*D/G)) over the fused decode
     kernel's mean launch time (the K back-to-back steps between events: one
     launch per step); the split pass alone (va_decode_splits) beside it;
+  * size-matched ceiling per row (va_probe_read_sized): the chunked read of
+    exactly that row's bytes per launch, on the decode grid (one or two
+    4-wave groups per CU), back to back over the same >= 2 GiB rotation; what
+    any kernel reading that many bytes per launch takes, launch gap, ramp and
+    tail included. `mbu_sized` = the row's GB/s over that read's GB/s;
   * launch floor (va_probe_launch): us per back-to-back launch of an empty
     kernel with the decode step's grid (reported as launch_floor_us); an
     upper bound on the per-step launch cost, since part of it overlaps a
@@ -484,6 +489,7 @@ def main() -> int:
         rows_spec.append((None, args.headline, args.L))
     stream = va.Stream()
     rows = []
+    sized = {}     # algorithmic bytes -> size-matched read ceiling (us, GB/s)
     for cfg, name, L in rows_spec:
         fmt = va.Fmt.parse(name)
         w = Workload(va, fmt, H, L, D, G, int(args.set_gib * 2**30), 256)
@@ -496,15 +502,20 @@ def main() -> int:
             w.free()
         nbytes = algo_bytes(fmt, H, L, D, G)
         gbs = nbytes / (t["mean_ms"] * 1e6)
+        if nbytes not in sized:
+            sized[nbytes] = va.probe_read_sized(nbytes, int(args.set_gib * 2**30), launches=max(20, args.steps))
+        sz_us, sz_gbs = sized[nbytes]
         r = {"config": cfg, "fmt": fmt.label, "L": L, "S": S,
              "ms": t["mean_ms"], "best_single_ms": t["best_ms"], "split_pass_ms": t["kernel_ms"],
              "tok_s": 1e3 / t["mean_ms"], "tok_s_best_single": 1e3 / t["best_ms"],
              "bytes": nbytes, "gbps": gbs, "mbu": gbs / ceiling, "pct_peak": gbs / PEAK_HBM_GBPS,
+             "sized_ceiling_us": sz_us, "sized_ceiling_gbps": sz_gbs, "mbu_sized": gbs / sz_gbs,
              "copies": w.copies, "working_set_bytes": w.copies * w.copy_bytes, **chk}
         rows.append(r)
         log(f"cfg[{'-' if cfg is None else cfg}] {fmt.label:5s} L={L:6d} S={S:3d} copies={w.copies:3d}  "
             f"mean {r['ms'] * 1e3:8.2f} us  best {r['best_single_ms'] * 1e3:8.2f} us  "
             f"{gbs:7.1f} GB/s  MBU {100 * r['mbu']:5.1f}%  peak {100 * r['pct_peak']:5.1f}%  "
+            f"sized read {sz_us:7.2f} us ({100 * r['mbu_sized']:5.1f}%)  "
             f"tok/s {r['tok_s']:8.0f}  check {'-' if r['checked'] is None else ('ok' if r['checked'] else 'FAIL')}")
     # vs f16 / vs f16+ at the same L
     for r in rows:
@@ -553,6 +564,7 @@ def main() -> int:
                 "kernel": f"decode_tiled<{args.headline}> fused (split-L pass + LSE merge, one launch per step)",
                 "algorithmic_bytes_per_launch": head["bytes"],
                 "kernel_ms": head["ms"], "frac_of_probed": step_gbs / ceiling,
+                "frac_of_sized_read": head["mbu_sized"], "sized_read_us": head["sized_ceiling_us"],
                 "split_pass_only_ms": head["split_pass_ms"],
                 "split_pass_only_gbps": head["bytes"] / (head["split_pass_ms"] * 1e6) if head["split_pass_ms"] > 0 else None}
     cpu = cpu0 = None
@@ -591,7 +603,7 @@ def main() -> int:
         "formats": formats,
         "configs": rows,
         "extra": extra,
-        "device": info["name"], "compute_units": info["compute_units"],
+        "device": info["name"] or info["arch"], "arch": info["arch"], "compute_units": info["compute_units"],
     }
     print(json.dumps(line), flush=True)
     if checked is False:

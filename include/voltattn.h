@@ -180,6 +180,32 @@ int va_fill_normal(float* x, size_t n, uint64_t seed, void* stream);
  * one contiguous chunk, the shape of a decode split; buffers of 16 MiB and up). */
 int va_probe_read(size_t bytes, int reps, double* best_gbps);
 
+/* One launch of a read-probe form of va_probe_read over the caller's device
+ * buffer, with a digest of what it read: xor4 = the XOR of every 16-byte word
+ * loaded (as four little-endian uint32), *loads = the 16-byte loads issued,
+ * *bytes_read = the bytes va_probe_read credits the form with (all of
+ * `bytes`, for both forms). form 0: the grid-stride read (read_kernel's shape,
+ * src/voltattn.cu:69-78): `grid` groups of 256 threads, unroll 2, 4 or 8 loads
+ * in flight per lane; form 1: the chunked read: `grid` groups of 256 threads,
+ * each streaming one contiguous chunk, unroll 4 or 8. bytes: a positive
+ * multiple of 16; src 16-byte aligned. Synchronous. A form that skipped,
+ * repeated or over-counted bytes does not reproduce the XOR and load count of
+ * the same bytes computed on the host. */
+int va_probe_digest(const void* src, size_t bytes, int form, int grid, int unroll, uint32_t* xor4,
+                    uint64_t* loads, size_t* bytes_read);
+
+/* Size-matched read ceiling of one decode step of `bytes`: the chunked read of
+ * va_probe_read over exactly `bytes` per launch with one or two 4-wave groups
+ * per CU (the decode grid), `launches` launches back to back on one stream
+ * between two events, rotating over copies that together span >= min_set
+ * bytes (so the Infinity Cache cannot serve them), after a warm-up; the best
+ * mean over the chunked shapes. Returns microseconds per launch and bytes /
+ * that time in GB/s: what any kernel that reads that many bytes per launch
+ * pays, launch gap, ramp and tail included. No counterpart in the reference
+ * (its probe reads one fixed 256 MiB buffer, src/voltattn.cu:935-957). */
+int va_probe_read_sized(size_t bytes, size_t min_set, int launches, double* us_per_launch,
+                        double* gbps);
+
 /* Launch floor: microseconds per launch of an empty kernel with one 256-thread
  * work-group per CU (the decode step's grid at H*S = CUs), `launches` of them
  * back to back on a private stream after a warm-up: an upper bound on the

@@ -164,3 +164,17 @@ def test_probe_argument_checks():
     assert va.lib.va_probe_launch(2000000, C.byref(d)) == VA_EINVAL
     assert va.lib.va_probe_read(1 << 30, 1, None) == VA_ENULL
     assert va.lib.va_probe_read(1024, 1, C.byref(d)) == VA_EINVAL       # below 1 MiB
+    # va_probe_digest / va_probe_read_sized: argument checks come before any device call
+    x = (C.c_uint32 * 4)()
+    n = C.c_uint64(0)
+    b = C.c_size_t(0)
+    assert va.lib.va_probe_digest(None, 4096, 0, 256, 4, x, C.byref(n), C.byref(b)) == VA_ENULL
+    assert va.lib.va_probe_digest(0x1000, 4096, 0, 256, 4, None, C.byref(n), C.byref(b)) == VA_ENULL
+    assert va.lib.va_probe_digest(0x1000, 4096, 2, 256, 4, x, C.byref(n), C.byref(b)) == VA_EINVAL
+    assert va.lib.va_probe_digest(0x1000, 4096, 1, 0, 4, x, C.byref(n), C.byref(b)) == VA_EINVAL
+    assert va.lib.va_probe_digest(0x1000, 4096, 1, 256, 2, x, C.byref(n), C.byref(b)) == VA_EINVAL
+    assert va.lib.va_probe_digest(0x1000, 4100, 0, 256, 4, x, C.byref(n), C.byref(b)) == VA_EINVAL
+    assert va.lib.va_probe_digest(0x1008, 4096, 0, 256, 4, x, C.byref(n), C.byref(b)) == VA_EALIGN
+    assert va.lib.va_probe_read_sized(1 << 20, 1 << 30, 10, None, C.byref(d)) == VA_ENULL
+    assert va.lib.va_probe_read_sized(1024, 1 << 30, 10, C.byref(d), C.byref(d)) == VA_EINVAL
+    assert va.lib.va_probe_read_sized(1 << 20, 1 << 30, 0, C.byref(d), C.byref(d)) == VA_EINVAL

@@ -54,3 +54,7 @@ def test_json_line_contract():
         assert k in cb, k
     assert cb["kind"] == "port" and cb["cores"] == 1 and cb["value"] > 0
     assert j["launch_floor_us"] > 0 and j["probed_ceiling_gbps"] > 0
+    assert j["device"]
+    for r in j["configs"]:
+        assert r["sized_ceiling_us"] > 0 and r["sized_ceiling_gbps"] > 0
+        assert abs(r["mbu_sized"] - r["gbps"] / r["sized_ceiling_gbps"]) < 1e-9

@@ -26,7 +26,7 @@ import numpy as np
 __all__ = [
     "Fmt", "DeviceBufs", "VAError", "launch", "decode_splits", "merge", "ws_bytes",
     "payload_bytes", "scale_bytes", "split_chunk", "pick_splits", "quantize", "dequantize", "f32_to_f16",
-    "fill_normal", "probe_read", "merge_faults", "device_info", "device_count", "DeviceBuffer", "Event",
+    "fill_normal", "probe_read", "probe_digest", "probe_read_sized", "merge_faults", "device_info", "device_count", "DeviceBuffer", "Event",
     "Stream", "Graph", "sync", "lib", "LIB_PATH", "fmt_bits", "is_f16", "check",
     "PagedShape", "PagedBufs", "decode_gqa", "pick_splits_gqa", "decode_paged",
     "pick_splits_paged", "page_bytes", "page_scale_bytes", "append_kv", "row_bytes",
@@ -108,6 +108,8 @@ _sig("va_f32_to_f16", _I, _P, _SZ, _P, _P)
 _sig("va_fill_normal", _I, _P, _SZ, _U64, _P)
 _sig("va_probe_read", _I, _SZ, _I, C.POINTER(C.c_double))
 _sig("va_probe_launch", _I, _I, C.POINTER(C.c_double))
+_sig("va_probe_digest", _I, _P, _SZ, _I, _I, _I, C.POINTER(C.c_uint32), C.POINTER(_U64), C.POINTER(_SZ))
+_sig("va_probe_read_sized", _I, _SZ, _SZ, _I, C.POINTER(C.c_double), C.POINTER(C.c_double))
 _sig("va_decode_gqa", _I, _I, C.POINTER(_Bufs), _I, _I, _I, _I, _I, _I, _P)
 _sig("va_pick_splits_gqa", _I, _I, _I, _I, _I, _I, C.POINTER(_I))
 _sig("va_decode_paged", _I, _I, C.POINTER(_PagedBufs), C.POINTER(_PagedShape), _I, _P)
@@ -359,6 +361,27 @@ def probe_read(nbytes: int, reps: int = 10) -> float:
     g = C.c_double(0.0)
     check(lib.va_probe_read(nbytes, reps, C.byref(g)))
     return g.value
+
+
+def probe_digest(src: int, nbytes: int, form: int, grid: int, unroll: int):
+    """va_probe_digest: one launch of read-probe form `form` (0 grid-stride,
+    1 chunked) over device buffer `src`; returns (xor of every 16-byte word read
+    as 16 bytes, number of 16-byte loads, bytes credited)."""
+    x = (C.c_uint32 * 4)()
+    n = _U64(0)
+    b = _SZ(0)
+    check(lib.va_probe_digest(src, nbytes, form, grid, unroll, x, C.byref(n), C.byref(b)))
+    import struct
+    return struct.pack("<4I", *x), n.value, b.value
+
+
+def probe_read_sized(nbytes: int, min_set: int = 2 << 30, launches: int = 50):
+    """va_probe_read_sized: (us per launch, GB/s) of the chunked read of exactly
+    `nbytes` per launch, back to back over copies spanning >= min_set bytes."""
+    us = C.c_double(0.0)
+    g = C.c_double(0.0)
+    check(lib.va_probe_read_sized(nbytes, min_set, launches, C.byref(us), C.byref(g)))
+    return us.value, g.value
 
 
 def probe_launch(launches: int = 2000) -> float:

@@ -101,15 +101,22 @@ hipError_t lost_merges_ex(unsigned* n);
 hipError_t launch_merge(const float* ws, uint16_t* out, int H, int D, int S,
                         hipStream_t stream);
 
-// Read-bandwidth probe kernel over `bytes` (multiple of 16) at `src`.
-hipError_t launch_probe(const void* src, size_t bytes, float* sink, int grid,
+// Read-bandwidth probes. Each launch writes one digest per work-group to
+// dig[g * PROBE_DIGEST_WORDS ..]: the XOR of every 16-byte word the group
+// loaded (4 words), then the number of 16-byte loads it issued.
+constexpr int PROBE_DIGEST_WORDS = 8;
+
+// Grid-stride probe over `bytes` (multiple of 16) at `src`.
+hipError_t launch_probe(const void* src, size_t bytes, uint32_t* dig, int grid,
                         int unroll, hipStream_t stream);
 
-// Chunked read probe: `grid` work-groups, each streaming a contiguous chunk of
-// whole 4096*unroll-byte tiles (unroll 4 or 8); the bytes it reads (a multiple
-// of grid * tile, at most `bytes`) go to *bytes_read.
-hipError_t launch_probe_chunks(const void* src, size_t bytes, float* sink, int grid, int unroll,
-                               hipStream_t stream, size_t* bytes_read);
+// Chunked probe: `grid` work-groups, group g streaming the contiguous chunk
+// [g*per, min(bytes, (g+1)*per)) with per = probe_chunk_bytes(bytes, grid),
+// unroll 4 or 8 loads per lane in flight; covers exactly `bytes` (a multiple
+// of 16, per < 2^31).
+size_t probe_chunk_bytes(size_t bytes, int grid);
+hipError_t launch_probe_chunks(const void* src, size_t bytes, uint32_t* dig, int grid, int unroll,
+                               hipStream_t stream);
 
 // Empty kernel of `grid` 256-thread groups (the launch-floor probe).
 hipError_t launch_empty(int grid, float* sink, hipStream_t stream);

@@ -17,6 +17,7 @@
 #include <cstring>
 #include <mutex>
 #include <unordered_map>
+#include <vector>
 
 namespace {
 
@@ -658,10 +659,16 @@ int va_probe_read(size_t bytes, int reps, double* best_gbps) {
     if (!best_gbps) return fail(VA_ENULL, "best_gbps is NULL");
     if (bytes < (1u << 20) || reps < 1) return fail(VA_EINVAL, "probe needs >= 1 MiB and reps >= 1");
     bytes &= ~(size_t)15;
+    const int cus = cu_count() > 0 ? cu_count() : 256;
+    const int grids[]   = {cus * 4, cus * 8, cus * 16, cus * 32};
+    const int unrolls[] = {4, 8};
     void* src = nullptr;
-    float* sink = nullptr;
+    uint32_t* dig = nullptr;
     VA_HIP(hipMalloc(&src, bytes), "hipMalloc probe buffer");
-    if (hipMalloc(&sink, 4) != hipSuccess) { (void)hipFree(src); return fail(VA_EHIP, "hipMalloc sink"); }
+    if (hipMalloc(&dig, (size_t)cus * 32 * va::PROBE_DIGEST_WORDS * 4) != hipSuccess) {
+        (void)hipFree(src);
+        return fail(VA_EHIP, "hipMalloc digest");
+    }
     int rc = VA_OK;
     hipEvent_t e0 = nullptr, e1 = nullptr;
     double best = 0.0;
@@ -672,50 +679,135 @@ int va_probe_read(size_t bytes, int reps, double* best_gbps) {
             rc = hip_fail(e, "hipEventCreate");
             break;
         }
-        const int cus = cu_count() > 0 ? cu_count() : 256;
-        const int grids[]   = {cus * 4, cus * 8, cus * 16, cus * 32};
-        const int unrolls[] = {4, 8};
-        for (int gsz : grids) {
-            for (int un : unrolls) {
-                if ((e = va::launch_probe(src, bytes, sink, gsz, un, nullptr)) != hipSuccess) break;
-                for (int r = 0; r < reps && e == hipSuccess; ++r) {
-                    (void)hipEventRecord(e0, nullptr);
-                    e = va::launch_probe(src, bytes, sink, gsz, un, nullptr);
-                    (void)hipEventRecord(e1, nullptr);
-                    if (e == hipSuccess) e = hipEventSynchronize(e1);
-                    float ms = 0.f;
-                    if (e == hipSuccess) e = hipEventElapsedTime(&ms, e0, e1);
-                    if (e == hipSuccess && ms > 0.f) best = std::max(best, (double)bytes / (ms * 1e6));
+        // Both forms read all `bytes` (va_probe_digest checks each form's coverage).
+        for (int form = 0; form < 2 && e == hipSuccess; ++form) {
+            for (int gi = 0; gi < (form == 0 ? 4 : 2) && e == hipSuccess; ++gi) {
+                const int gsz = form == 0 ? grids[gi] : cus * (gi + 1);   // chunked: 1 or 2 groups per CU
+                for (int un : unrolls) {
+                    auto launch = [&]() {
+                        return form == 0 ? va::launch_probe(src, bytes, dig, gsz, un, nullptr)
+                                         : va::launch_probe_chunks(src, bytes, dig, gsz, un, nullptr);
+                    };
+                    if ((e = launch()) != hipSuccess) break;
+                    for (int r = 0; r < reps && e == hipSuccess; ++r) {
+                        (void)hipEventRecord(e0, nullptr);
+                        e = launch();
+                        (void)hipEventRecord(e1, nullptr);
+                        if (e == hipSuccess) e = hipEventSynchronize(e1);
+                        float ms = 0.f;
+                        if (e == hipSuccess) e = hipEventElapsedTime(&ms, e0, e1);
+                        if (e == hipSuccess && ms > 0.f) best = std::max(best, (double)bytes / (ms * 1e6));
+                    }
+                    if (e != hipSuccess) break;
                 }
-                if (e != hipSuccess) break;
-            }
-            if (e != hipSuccess) break;
-        }
-        // the chunked form: one or two 4-wave groups per CU, 4 or 8 loads per lane in flight
-        for (int gpc = 1; gpc <= 2 && e == hipSuccess; ++gpc) {
-            for (int un : unrolls) {
-                if (bytes / ((size_t)4096 * un) / (size_t)(cus * gpc) == 0) continue;   // buffer too small
-                size_t nread = 0;
-                if ((e = va::launch_probe_chunks(src, bytes, sink, cus * gpc, un, nullptr, &nread)) != hipSuccess) break;
-                for (int r = 0; r < reps && e == hipSuccess; ++r) {
-                    (void)hipEventRecord(e0, nullptr);
-                    e = va::launch_probe_chunks(src, bytes, sink, cus * gpc, un, nullptr, &nread);
-                    (void)hipEventRecord(e1, nullptr);
-                    if (e == hipSuccess) e = hipEventSynchronize(e1);
-                    float ms = 0.f;
-                    if (e == hipSuccess) e = hipEventElapsedTime(&ms, e0, e1);
-                    if (e == hipSuccess && ms > 0.f) best = std::max(best, (double)nread / (ms * 1e6));
-                }
-                if (e != hipSuccess) break;
             }
         }
         if (e != hipSuccess) rc = hip_fail(e, "probe");
     } while (0);
     if (e0) (void)hipEventDestroy(e0);
     if (e1) (void)hipEventDestroy(e1);
-    (void)hipFree(sink);
+    (void)hipFree(dig);
     (void)hipFree(src);
     if (rc == VA_OK) *best_gbps = best;
+    return rc;
+}
+
+int va_probe_digest(const void* src, size_t bytes, int form, int grid, int unroll, uint32_t* xor4,
+                    uint64_t* loads, size_t* bytes_read) {
+    if (!src || !xor4 || !loads || !bytes_read) return fail(VA_ENULL, "src, xor4, loads and bytes_read must be non-NULL");
+    if (form != 0 && form != 1) return fail(VA_EINVAL, "form must be 0 (grid-stride) or 1 (chunked)");
+    if (grid < 1 || grid > 65536) return fail(VA_EINVAL, "grid must be in [1, 65536] (got %d)", grid);
+    if (unroll != 4 && unroll != 8 && !(form == 0 && unroll == 2))
+        return fail(VA_EINVAL, "unroll must be 4 or 8 (2 also for the grid-stride form)");
+    if (bytes == 0 || bytes % 16) return fail(VA_EINVAL, "bytes must be a positive multiple of 16");
+    if (!aligned(src, 16)) return fail(VA_EALIGN, "src must be 16-byte aligned");
+    if (form == 1 && va::probe_chunk_bytes(bytes, grid) > 0x7FFFFFFFu)
+        return fail(VA_ERANGE, "chunk per work-group must stay below 2^31 bytes");
+    uint32_t* dig = nullptr;
+    const size_t dwords = (size_t)grid * va::PROBE_DIGEST_WORDS;
+    VA_HIP(hipMalloc(&dig, dwords * 4), "hipMalloc digest");
+    std::vector<uint32_t> h(dwords);
+    hipError_t e = form == 0 ? va::launch_probe(src, bytes, dig, grid, unroll, nullptr)
+                             : va::launch_probe_chunks(src, bytes, dig, grid, unroll, nullptr);
+    if (e == hipSuccess) e = hipDeviceSynchronize();
+    if (e == hipSuccess) e = hipMemcpy(h.data(), dig, dwords * 4, hipMemcpyDeviceToHost);
+    (void)hipFree(dig);
+    if (e != hipSuccess) return hip_fail(e, "probe digest");
+    uint32_t x[4] = {0, 0, 0, 0};
+    uint64_t n = 0;
+    for (int g = 0; g < grid; ++g) {
+        const uint32_t* d = h.data() + (size_t)g * va::PROBE_DIGEST_WORDS;
+        for (int i = 0; i < 4; ++i) x[i] ^= d[i];
+        n += d[4];
+    }
+    for (int i = 0; i < 4; ++i) xor4[i] = x[i];
+    *loads = n;
+    *bytes_read = bytes;
+    return VA_OK;
+}
+
+int va_probe_read_sized(size_t bytes, size_t min_set, int launches, double* us_per_launch, double* gbps) {
+    if (!us_per_launch || !gbps) return fail(VA_ENULL, "us_per_launch and gbps must be non-NULL");
+    bytes &= ~(size_t)15;
+    if (bytes < 4096 || launches < 1 || launches > 100000)
+        return fail(VA_EINVAL, "sized probe needs >= 4096 bytes and launches in [1, 10^5]");
+    const int cus = cu_count() > 0 ? cu_count() : 256;
+    if (va::probe_chunk_bytes(bytes, cus) > 0x7FFFFFFFu) return fail(VA_ERANGE, "bytes too large for the chunked probe");
+    const size_t stride = (bytes + 4095) & ~(size_t)4095;
+    const size_t copies = std::max<size_t>(1, std::min<size_t>(4096, (min_set + stride - 1) / stride));
+    void* src = nullptr;
+    uint32_t* dig = nullptr;
+    VA_HIP(hipMalloc(&src, copies * stride), "hipMalloc sized probe buffer");
+    if (hipMalloc(&dig, (size_t)cus * 2 * va::PROBE_DIGEST_WORDS * 4) != hipSuccess) {
+        (void)hipFree(src);
+        return fail(VA_EHIP, "hipMalloc digest");
+    }
+    hipStream_t st = nullptr;
+    hipEvent_t e0 = nullptr, e1 = nullptr;
+    int rc = VA_OK;
+    double best_ms = 0.0;
+    do {
+        hipError_t e;
+        if ((e = hipMemset(src, 1, copies * stride)) != hipSuccess) { rc = hip_fail(e, "hipMemset"); break; }
+        if ((e = hipStreamCreateWithFlags(&st, hipStreamNonBlocking)) != hipSuccess) { rc = hip_fail(e, "hipStreamCreate"); break; }
+        if ((e = hipEventCreate(&e0)) != hipSuccess || (e = hipEventCreate(&e1)) != hipSuccess) {
+            rc = hip_fail(e, "hipEventCreate");
+            break;
+        }
+        // The chunked form's four shapes (1 or 2 groups per CU, 4 or 8 loads per
+        // lane in flight), each `launches` back to back over rotating copies;
+        // the best mean is the ceiling.
+        for (int gpc = 1; gpc <= 2 && e == hipSuccess; ++gpc) {
+            for (int un : {4, 8}) {
+                size_t c = 0;
+                auto launch = [&]() {
+                    const void* p = static_cast<const uint8_t*>(src) + (c++ % copies) * stride;
+                    return va::launch_probe_chunks(p, bytes, dig, cus * gpc, un, st);
+                };
+                for (int i = 0; i < 5 && e == hipSuccess; ++i) e = launch();
+                if (e == hipSuccess) e = hipStreamSynchronize(st);
+                if (e == hipSuccess) e = hipEventRecord(e0, st);
+                for (int i = 0; i < launches && e == hipSuccess; ++i) e = launch();
+                if (e == hipSuccess) e = hipEventRecord(e1, st);
+                if (e == hipSuccess) e = hipEventSynchronize(e1);
+                float ms = 0.f;
+                if (e == hipSuccess) e = hipEventElapsedTime(&ms, e0, e1);
+                if (e != hipSuccess) break;
+                const double per = (double)ms / launches;
+                if (per > 0.0 && (best_ms == 0.0 || per < best_ms)) best_ms = per;
+            }
+        }
+        if (e != hipSuccess) rc = hip_fail(e, "sized probe");
+    } while (0);
+    if (e0) (void)hipEventDestroy(e0);
+    if (e1) (void)hipEventDestroy(e1);
+    if (st) (void)hipStreamDestroy(st);
+    (void)hipFree(dig);
+    (void)hipFree(src);
+    if (rc == VA_OK) {
+        *us_per_launch = best_ms * 1e3;
+        *gbps = best_ms > 0.0 ? (double)bytes / (best_ms * 1e6) : 0.0;
+    }
     return rc;
 }
 
