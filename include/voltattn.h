@@ -35,7 +35,7 @@
 extern "C" {
 #endif
 
-#define VA_ABI_VERSION 3
+#define VA_ABI_VERSION 4
 
 /* Status codes. */
 enum {
@@ -46,7 +46,8 @@ enum {
     VA_ERANGE   = 4,  /* shape exceeds the 32-bit buffer addressing of a head */
     VA_EHIP     = 5,  /* HIP runtime or launch error */
     VA_ENODEV   = 6,  /* no usable gfx950 device */
-    VA_ELOST    = 7   /* a fused merge gave up waiting for a partial (va_merge_faults) */
+    VA_ELOST    = 7,  /* a fused merge gave up waiting for a partial (va_merge_faults) */
+    VA_EBUSY    = 8   /* va_decode_noalloc: the device's workspace is bound to another stream */
 };
 
 /* Formats: the reference's enum class Fmt {F16, F16M, Q8, Q8M, Q4, Q4M, Q3M}
@@ -95,8 +96,12 @@ typedef struct {
  * and capture sequence while a graph is captured; 16 per device). Calls on
  * different streams may run concurrently; replays of one captured graph must
  * be ordered after each other (as every launch of one executable graph is).
- * With H > 1024, S > 64, H*S > 2048, or all 16 slots bound to other streams,
- * the partials go to ws and a separate merge kernel follows. */
+ * When all 16 slots are bound, an eager call may take over the slot of
+ * another eager stream that has finished its work; slots of captured graphs
+ * are kept until va_graph_destroy or va_capture_release. With H > 1024,
+ * S > 64, H*S > 2048, no slot to be had, or the per-thread default stream
+ * (hipStreamPerThread, one handle naming a stream per host thread), the
+ * partials go to ws and a separate merge kernel follows. */
 int va_decode(va_fmt fmt, const va_bufs* b, int H, int L, int D, int G, int S, void* stream);
 
 /* va_decode without a workspace argument, for callers that cannot allocate
@@ -105,10 +110,30 @@ int va_decode(va_fmt fmt, const va_bufs* b, int H, int L, int D, int G, int S, v
  * form's partials go to a workspace of library device memory (4 MiB per
  * device, held until the process ends), so H*S*(D+2) must not exceed
  * VA_NOALLOC_MAX_FLOATS (VA_ERANGE otherwise). Allocates nothing; same
- * kernels and outputs as va_decode. Every call on a device shares that
- * device's workspace: calls that overlap on one device race. */
+ * kernels and outputs as va_decode. The fused merge (va_decode) uses no
+ * workspace; the two-pass form binds the device's workspace to the calling
+ * stream (or stream and capture sequence; for hipStreamPerThread, the calling
+ * thread) as ticket slots are bound: another owner's two-pass call returns
+ * VA_EBUSY, unless the owner is an eager stream that has finished its work
+ * (the binding then moves). Calls never share the workspace while they may
+ * overlap. va_stream_release / va_capture_release free the binding. */
 #define VA_NOALLOC_MAX_FLOATS 1048576
 int va_decode_noalloc(va_fmt fmt, const va_bufs* b, int H, int L, int D, int G, int S, void* stream);
+
+/* Release what `stream` holds on the current device: its fused-merge ticket
+ * slot and its binding of the allocation-free workspace (for
+ * hipStreamPerThread, the calling thread's), after waiting for the stream's
+ * work. For streams the library did not create (va_stream_destroy releases
+ * its own), before they are destroyed or when they stop decoding. No
+ * counterpart in the reference, which launches on the default stream only. */
+int va_stream_release(void* stream);
+
+/* Release the ticket slots and workspace binding of a graph capture sequence
+ * (the id hipStreamGetCaptureInfo reported while capturing), after waiting for
+ * the device: for graphs captured outside va_graph_begin/end (which
+ * va_graph_destroy releases), once they will not be replayed again. No
+ * counterpart in the reference. */
+int va_capture_release(unsigned long long capture_id);
 
 /* Fused merges on the current device that gave up waiting for a partial
  * (bounded poll exhausted; the affected outputs were set to NaN) since the

@@ -114,3 +114,41 @@ def test_fuzz_paged(case):
     finally:
         pb.free()
     _check(got, pb.ref, what, pb.mag)
+
+
+def test_cancelling_grouped_case():
+    """A fixed grouped-query case whose outputs cancel ~1800x below the terms
+    summed into them (q4+, Hq 7 over Hkv 1, L 16, S 24: draw 503 of the
+    generator above, found by an extended sweep). Every fp32 kernel rounds at
+    the scale of those terms: an ideal one (exact dots, fp32 scores, exp2 and
+    sequential sums) lands at 0.99 of the plain fp16 rounding bound here, and
+    this kernel's split and lane order just over it. So the plain bound fails
+    and the widened one (cond_bound: 8 fp32 ulps of sum_j p_j |v_jd|) holds."""
+    from tests.numerics import tight_bound
+    case, fmt, Hkv, Hq, L, D, G, S = 503, va.Fmt.Q4M, 1, 7, 16, 128, 32, 24
+    print("cancelling case", case, flush=True)
+    c = batch_util.kv_case(fmt, Hkv, L, D, G, 0xB000 + case)
+    q = batch_util.queries(Hq, D, 0xB100 + case)
+    bufs = []
+    try:
+        dev = lambda a: bufs.append(va.DeviceBuffer.from_array(a)) or bufs[-1].ptr
+        out = va.DeviceBuffer(Hq * D * 2)
+        ws = va.DeviceBuffer(va.ws_bytes(Hq, D, S))
+        bufs += [out, ws]
+        b = va.DeviceBufs(K=dev(c["kpay"]), V=dev(c["vpay"]), scK=dev(c["ksc"]), scV=dev(c["vsc"]),
+                          q=dev(q), out=out.ptr, ws=ws.ptr)
+        va.decode_gqa(fmt, b, Hq, Hkv, L, D, S=S, G=G)
+        va.sync()
+        got = out.download(np.uint16).view(np.float16).astype(np.float64).ravel()
+    finally:
+        for x in bufs:
+            x.free()
+    ref = batch.reference_gqa(c["kd"], c["vd"], q, Hq, Hkv, L, D).astype(np.float64).ravel()
+    mag = np.asarray(batch.magnitude_gqa(c["kd"], c["vd"], q, Hq, Hkv, L, D), np.float64).ravel()
+    err = np.abs(got - ref)
+    r_tight = float(np.max(err / tight_bound(ref)))
+    r_cond = float(np.max(err / cond_bound(ref, mag)))
+    print(f"ratio to the plain bound {r_tight:.3f}, to cond_bound {r_cond:.3f}, "
+          f"max cancellation {float(np.max(mag / np.maximum(np.abs(ref), 1e-30))):.0f}", flush=True)
+    assert r_cond <= 1.0
+    assert r_tight > 1.0

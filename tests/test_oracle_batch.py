@@ -120,3 +120,36 @@ def test_magnitude_bounds_the_reference_and_closed_forms():
     # one position: the weight is 1, so the magnitude is |v_0| exactly
     mag1 = batch.magnitude_gqa(kd[:, :1], vd[:, :1], q, Hq, Hkv, 1, D).reshape(Hq, D)
     np.testing.assert_array_equal(mag1, np.abs(np.repeat(vd[:, 0], Hq // Hkv, axis=0)).astype(np.float64))
+
+
+def test_cancelling_case_has_no_headroom_under_the_plain_bound():
+    """The fixed grouped case of tests/test_gpu_fuzz.py::test_cancelling_grouped_case
+    (q4+, Hq 7 over Hkv 1, L 16): an ideal fp32 kernel (exact dot products,
+    fp32 scores in log2 units, fp32 exp2, sequential fp32 sums, fp16 output)
+    already lands within 5% of the plain fp16 rounding bound, because outputs
+    cancel >1000x below sum_j p_j |v_jd|; cond_bound's widening (8 fp32 ulps of
+    that magnitude) is what any fp32 summation order needs there."""
+    import voltattn_amd as va
+    from tests import batch_util
+    from tests.numerics import cond_bound, tight_bound
+    case, fmt, Hkv, Hq, L, D, G = 503, va.Fmt.Q4M, 1, 7, 16, 128, 32
+    c = batch_util.kv_case(fmt, Hkv, L, D, G, 0xB000 + case)
+    q = batch_util.queries(Hq, D, 0xB100 + case)
+    ref = batch.reference_gqa(c["kd"], c["vd"], q, Hq, Hkv, L, D).astype(np.float64).reshape(Hq, D)
+    mag = np.asarray(batch.magnitude_gqa(c["kd"], c["vd"], q, Hq, Hkv, L, D), np.float64).reshape(Hq, D)
+    kd = c["kd"].reshape(L, D).astype(np.float64)
+    vd = c["vd"].reshape(L, D).astype(np.float32)
+    qq = q.view(np.float16).reshape(Hq, D).astype(np.float64)
+    out = np.zeros((Hq, D))
+    for h in range(Hq):
+        s2 = (kd @ qq[h] * (np.log2(np.e) / np.sqrt(D))).astype(np.float32)
+        p = np.exp2(s2 - s2.max()).astype(np.float32)
+        l, o = np.float32(0), np.zeros(D, np.float32)
+        for j in range(L):
+            l = np.float32(l + p[j])
+            o = (o + p[j] * vd[j]).astype(np.float32)
+        out[h] = (o / l).astype(np.float16)
+    ratio = np.max(np.abs(out - ref) / tight_bound(ref))
+    assert 0.95 < ratio <= 1.0
+    assert np.max(mag / np.maximum(np.abs(ref), 1e-30)) > 1000
+    assert np.all(np.abs(out - ref) <= cond_bound(ref, mag))

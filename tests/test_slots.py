@@ -5,8 +5,11 @@ on different streams (or a captured graph and anything else) must not. The
 binding logic is plain C++, so tests/cpp/test_slots.cpp drives it directly:
 one slot per eager stream, one per (stream, capture sequence), distinct
 slots across streams and captures, per-device tables, -1 (two-pass form) once
-a device's 16 slots are bound, and distinct slots under concurrent first
-calls from 16 threads."""
+a device's 16 slots are bound and none can be taken over, distinct slots under
+concurrent first calls from 16 threads; a take-over only of an idle eager
+owner with no call between acquire() and done(), never of a capture's slot;
+call counters that outlive bindings; and, under concurrent take-overs by 8
+threads sharing 2 slots, never two calls holding one slot."""
 import subprocess
 import tempfile
 from pathlib import Path

@@ -159,3 +159,61 @@ def test_dequantize_rejects_bad_arguments():
         torch.ops.voltattn.dequantize(_t(4, 64), _t(4, 2, dtype=torch.float16), 4, 32)
     with pytest.raises(RuntimeError, match="scales has dtype"):
         torch.ops.voltattn.dequantize(_t(4, 64), _t(4, 4, dtype=torch.float32), 4, 32)
+
+
+def _traced_guards(fn, *args):
+    """Guards and symbol values recorded while tracing fn with symbolic shapes."""
+    from torch.fx.experimental.proxy_tensor import make_fx
+    gm = make_fx(fn, tracing_mode="symbolic")(*args)
+    for n in gm.graph.nodes:
+        v = n.meta.get("val")
+        if hasattr(v, "fake_mode"):
+            se = v.fake_mode.shape_env
+            return [g.expr for g in se.guards], {k: int(x) for k, x in se.var_to_val.items()}
+    raise AssertionError("no fake values traced")
+
+
+def _free_of(guards, values, sizes):
+    """No guard mentions a symbol whose traced value is one of `sizes` (which
+    the inputs use only for batch, heads, positions, pages or rows)."""
+    syms = {s for s, x in values.items() if x in sizes}
+    bad = [g for g in guards if g.free_symbols & syms]
+    assert not bad, bad
+
+
+# Distinct sizes, none equal to D (128), D/G (4) or a row width, so that no
+# size shares a symbol with another under duck sizing.
+def test_symbolic_shapes_stay_symbolic():
+    H, Hkv, L, G = 6, 2, 1000, 32
+    q = torch.zeros(H, 128, dtype=torch.float16)
+    k = torch.zeros(H, L, 128, dtype=torch.uint8)
+    ks = torch.zeros(H, L, 4, dtype=torch.float16)
+    g, v = _traced_guards(lambda q, k, v, ks, vs: torch.ops.voltattn.decode(q, k, v, ks, vs, "q8+", G, 0),
+                          q, k, k.clone(), ks, ks.clone())
+    _free_of(g, v, {H, L})
+    k2 = torch.zeros(Hkv, L, 64, dtype=torch.uint8)
+    ks2 = torch.zeros(Hkv, L, 4, dtype=torch.float16)
+    g, v = _traced_guards(lambda q, k, v, ks, vs: torch.ops.voltattn.decode_gqa(q, k, v, ks, vs, "q4+", G, 0),
+                          q, k2, k2.clone(), ks2, ks2.clone())
+    _free_of(g, v, {L})                              # H and Hkv: only their divisibility is asserted
+    assert not [x for x in g if x.free_symbols and all(str(s) in {str(t) for t, y in v.items() if y == H}
+                                                      for s in x.free_symbols)]
+    B, P, PR, MP = 3, 10, 256, 5
+    qb = torch.zeros(B, H, 128, dtype=torch.float16)
+    kp = torch.zeros(P, Hkv, PR, 48, dtype=torch.uint8)
+    ksp = torch.zeros(P, Hkv, PR, 4, dtype=torch.float16)
+    bt = torch.zeros(B, MP, dtype=torch.int32)
+    sl = torch.zeros(B, dtype=torch.int32)
+    g, v = _traced_guards(lambda *a: torch.ops.voltattn.decode_paged(*a, "q3+", 1280, G, 0),
+                          qb, kp, kp.clone(), ksp, ksp.clone(), bt, sl)
+    _free_of(g, v, {B, P, PR, MP})
+    x = torch.zeros(B, Hkv, 7, 128, dtype=torch.float16)
+    st = torch.zeros(B, dtype=torch.int32)
+    kp8 = torch.zeros(P, Hkv, PR, 128, dtype=torch.uint8)
+    g, v = _traced_guards(lambda *a: torch.ops.voltattn.append_kv(*a, "q8+", G), x, st, bt, kp8, ksp)
+    _free_of(g, v, {B, P, PR, MP, 7})
+    g, v = _traced_guards(lambda x: torch.ops.voltattn.quantize(x, 4, G), torch.zeros(5, 9, 128))
+    _free_of(g, v, {5, 9})
+    g, v = _traced_guards(lambda p, s: torch.ops.voltattn.dequantize(p, s, 3, G),
+                          torch.zeros(5, 9, 48, dtype=torch.uint8), torch.zeros(5, 9, 4, dtype=torch.float16))
+    _free_of(g, v, {5, 9})

@@ -8,8 +8,19 @@ calls with the second smaller than the first, both in the fused form (merge
 inside the decode kernel; the workspace is unused) and in the two-pass form
 (S > 64: partials through the library workspace, then the merge kernel), and
 inside the reference's gate against the oracle. Shapes whose partials exceed
-the workspace are refused with VA_ERANGE before any device work."""
+the workspace are refused with VA_ERANGE before any device work.
+
+The workspace has one owner at a time (tests/noalloc_child.py, in a fresh
+process so that every ticket slot can be bound by captured graphs and the
+two-pass form is forced at S <= 64): another stream's call is refused with
+VA_EBUSY while the owner's work may still run, the binding moves once the
+owner is idle (eager streams) or released (per-thread streams, captures), and
+every output stays exact."""
 import ctypes as C
+import os
+import subprocess
+import sys
+from pathlib import Path
 
 import numpy as np
 import pytest
@@ -76,3 +87,15 @@ def test_noalloc_refuses_oversized_workspace():
     rc = va.lib.va_decode_noalloc(int(va.Fmt.Q8M), C.byref(cb), H, 4096, D, 32, S, None)
     assert rc == 4, va.lib.va_last_error()        # VA_ERANGE
     assert b"exceeds the allocation-free workspace" in va.lib.va_last_error()
+
+
+def test_noalloc_workspace_has_one_owner():
+    env = dict(os.environ)
+    env.pop("VOLTATTN_HIP_RUNTIME", None)          # the child uses no torch
+    root = Path(__file__).resolve().parent.parent
+    print("noalloc workspace ownership (child process)", flush=True)
+    r = subprocess.run([sys.executable, "-u", str(root / "tests" / "noalloc_child.py")], cwd=root, env=env,
+                       capture_output=True, text=True, timeout=110)
+    print(r.stdout[-3000:], flush=True)
+    assert r.returncode == 0, r.stderr[-3000:]
+    assert "noalloc child: ok" in r.stdout

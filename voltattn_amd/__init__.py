@@ -130,6 +130,8 @@ _sig("va_sync", _I)
 _sig("va_stream_create", _I, C.POINTER(_P))
 _sig("va_stream_destroy", _I, _P)
 _sig("va_stream_sync", _I, _P)
+_sig("va_stream_release", _I, _P)
+_sig("va_capture_release", _I, C.c_ulonglong)
 _sig("va_event_create", _I, C.POINTER(_P))
 _sig("va_event_destroy", _I, _P)
 _sig("va_event_record", _I, _P, _P)

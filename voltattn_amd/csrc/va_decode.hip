@@ -223,5 +223,6 @@ hipError_t launch_decode(int kind, bool tiled, int H, int D, int G, const Decode
 }
 
 hipError_t lost_merges_decode(unsigned* n) { return read_lost_merges(n); }
+hipError_t clear_tagged_decode(int slot, hipStream_t stream) { return launch_clear_tagged(slot, stream); }
 
 } // namespace va

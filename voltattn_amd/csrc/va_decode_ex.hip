@@ -200,5 +200,6 @@ hipError_t launch_decode_ex(int kind, int D, int G, int qg, bool paged, int grou
 }
 
 hipError_t lost_merges_ex(unsigned* n) { return read_lost_merges(n); }
+hipError_t clear_tagged_ex(int slot, hipStream_t stream) { return launch_clear_tagged(slot, stream); }
 
 } // namespace va

@@ -45,6 +45,24 @@ __device__ __forceinline__ void count_lost_merge() {
     __hip_atomic_fetch_add(&g_lost_merges, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// Tag of this call's partial words (va_kernels.hpp, TAG_EPOCH_BITS).
+__device__ __forceinline__ uint32_t part_tag(unsigned epoch, int S) {
+    return ((epoch & ((1u << TAG_EPOCH_BITS) - 1u)) << 7) | (uint32_t)S;
+}
+
+// Zero one slot's tagged partials (tag 0 is never current); a grid-stride
+// fill kernel rather than a memset, so it may sit in a captured graph.
+static __global__ __launch_bounds__(256) void clear_tagged_slot(int slot) {
+    constexpr size_t N = (size_t)PART_CAP * PART_STRIDE;
+    uint64_t* p = g_parts + (size_t)slot * N;
+    for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < N; i += (size_t)gridDim.x * 256) p[i] = 0;
+}
+static inline hipError_t launch_clear_tagged(int slot, hipStream_t stream) {
+    if (slot < 0 || slot >= TICKET_SLOTS) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(clear_tagged_slot, dim3(256), dim3(256), 0, stream, slot);
+    return hipGetLastError();
+}
+
 __device__ __forceinline__ uint64_t tagged(float v, uint32_t tag) {
     return ((uint64_t)tag << 32) | __builtin_bit_cast(uint32_t, v);
 }
@@ -93,8 +111,9 @@ struct Route {
 // L 65536, and 0.1-0.4 us more per one-slot step.
 
 // Tagged protocol: every value of a partial is stored as one 64-bit word
-// (tag << 32 | fp32 bits), tag = (epoch << 11 | mg << 1 | 1), unique per merge
-// group and call and never zero; a partial is PART_STRIDE words: m, l,
+// (tag << 32 | fp32 bits), tag = part_tag(epoch, S), never zero and, among the
+// words ever stored at that address, current only for this call
+// (va_kernels.hpp, TAG_EPOCH_BITS); a partial is PART_STRIDE words: m, l,
 // o[0..D), and partial (q, s) of merge group mg sits at (mg*QG + q)*S + s.
 // Thread NT-1 (which stores nothing, so its wait covers only its own atomic)
 // takes the group's ticket without waiting for the stores to complete; the
@@ -139,7 +158,7 @@ __device__ void finish_tagged(const DecodeArgs& a, const Route& rt, const float 
     if (t == NT - 1)
         s_last = __hip_atomic_fetch_add(ticket, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
                  (unsigned)(S - 1);
-    const uint32_t tag = (epoch << 11) | ((uint32_t)rt.mg << 1) | 1u;
+    const uint32_t tag = part_tag(epoch, S);
     const uint32_t want = VA_TEST_LOSE_MERGES ? tag ^ 0x80000000u : tag;   // the merger's expected tag
     uint64_t* base = g_parts + ((size_t)a.ticket_slot * PART_CAP + (size_t)rt.mg * QG * S) * PART_STRIDE;
     if (t < D) {

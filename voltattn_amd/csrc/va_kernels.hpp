@@ -60,6 +60,18 @@ constexpr int PART_CAP      = 2048; // partials (merge groups x QG x S) per slot
 constexpr int PART_STRIDE   = 130;  // 64-bit words per partial: m, l, o[D], D <= 128
 constexpr int PARTF_STRIDE  = 132;  // floats per plain partial: o[D], m, l (16-byte rows), D <= 128
 
+// Tags of the one-slot merge's partial words: (epoch mod 2^TAG_EPOCH_BITS) << 7
+// | S, S in [1, 64], so a tag is never 0 (the cleared state). Within one S the
+// word address fixes the merge group and split, so a word written under
+// another S never matches; a word of the same group and split written
+// 2^TAG_EPOCH_BITS of the group's calls earlier would, which the host rules
+// out by clearing a slot's store (clear_tagged_*) when it changes owner and
+// after every SLOT_CLEAR_CALLS eager calls on it. A captured graph's slot is
+// replayed with the split counts of its capture, so every word it reads was
+// written by the previous call of the same group and S.
+constexpr int TAG_EPOCH_BITS = 25;
+constexpr unsigned long long SLOT_CLEAR_CALLS = 1ull << (TAG_EPOCH_BITS - 1);
+
 // Page ids of one split of the paged kernels are staged in LDS: a split may
 // span at most this many pages.
 constexpr int MAX_SPLIT_PAGES = 1024;
@@ -96,6 +108,12 @@ int tile_positions(int kind, bool tiled, int D);
 // (va_decode_ex.hip). The counters only grow.
 hipError_t lost_merges_decode(unsigned* n);
 hipError_t lost_merges_ex(unsigned* n);
+
+// Zero the tagged partial store of ticket slot `slot` in the code object of the
+// reference-shape kernels (va_decode.hip) and of the grouped/paged kernels
+// (va_decode_ex.hip), on `stream`.
+hipError_t clear_tagged_decode(int slot, hipStream_t stream);
+hipError_t clear_tagged_ex(int slot, hipStream_t stream);
 
 // Second pass: log-sum-exp merge of the S partials of every head, fp16 out.
 hipError_t launch_merge(const float* ws, uint16_t* out, int H, int D, int S,

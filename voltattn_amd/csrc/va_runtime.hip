@@ -92,22 +92,132 @@ int validate(va_fmt fmt, const va_bufs* b, int H, int L, int D, int G, int S, bo
 }
 
 va::SlotTable<va::TICKET_SLOTS> g_slots;
+// Owner of the allocation-free entry point's workspace on each device.
+va::SlotTable<1> g_scratch_owner;
 // Capture sequence of each graph made by va_graph_end (its slots are released
 // by va_graph_destroy).
 std::mutex g_graph_mu;
 std::unordered_map<void*, unsigned long long> g_graph_capture;
 
-// Ticket slot of a fused call on `stream` (va_slots.hpp: one per eager stream,
-// one per stream and capture sequence while capturing), or -1: no slot free,
-// the call runs the two-pass form.
-int ticket_slot_for(void* stream) {
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess) return -1;
+// Owner key of `stream` for the calling thread: the handle, except for the
+// per-thread default stream (hipStreamPerThread), one handle that names a
+// different stream on each host thread, whose key is an odd address private
+// to the thread (never a stream handle, which is aligned).
+thread_local char g_thread_tag;
+uintptr_t owner_key(void* stream) {
+    if (as_stream(stream) == hipStreamPerThread) return reinterpret_cast<uintptr_t>(&g_thread_tag) | 1u;
+    return reinterpret_cast<uintptr_t>(stream);
+}
+
+// Capture sequence of `stream` (0: not capturing); false if HIP cannot tell.
+bool capture_of(void* stream, unsigned long long* capture) {
     hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
     unsigned long long id = 0;
-    if (hipStreamGetCaptureInfo(as_stream(stream), &cs, &id) != hipSuccess) return -1;
-    const unsigned long long capture = cs == hipStreamCaptureStatusActive ? (id | (1ull << 63)) : 0ull;
-    return g_slots.acquire(dev, reinterpret_cast<uintptr_t>(stream), capture);
+    if (hipStreamGetCaptureInfo(as_stream(stream), &cs, &id) != hipSuccess) return false;
+    *capture = cs == hipStreamCaptureStatusActive ? (id | (1ull << 63)) : 0ull;
+    return true;
+}
+
+// Whether an eager owner's stream has completed all its work, asked when a
+// binding is to be taken over. Per-thread keys are never asked about (another
+// thread's per-thread stream cannot be named). The query runs in relaxed
+// capture mode, and never on a stream that is capturing, so it cannot
+// disturb a capture in progress on this or another thread.
+bool owner_idle(uintptr_t key) {
+    if (key & 1u) return false;
+    const hipStream_t st = reinterpret_cast<hipStream_t>(key);
+    hipStreamCaptureMode mode = hipStreamCaptureModeRelaxed;
+    if (hipThreadExchangeStreamCaptureMode(&mode) != hipSuccess) return false;
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusActive;
+    const bool idle = hipStreamIsCapturing(st, &cs) == hipSuccess && cs == hipStreamCaptureStatusNone &&
+                      hipStreamQuery(st) == hipSuccess;
+    (void)hipThreadExchangeStreamCaptureMode(&mode);
+    return idle;
+}
+
+// Zero one ticket slot's tagged partials in both code objects, on `stream`.
+hipError_t clear_slot(int slot, hipStream_t stream) {
+    hipError_t e = va::clear_tagged_decode(slot, stream);
+    if (e == hipSuccess) e = va::clear_tagged_ex(slot, stream);
+    return e;
+}
+
+// A binding held by one call: the slot (or -1) and its owner; done() once the
+// call's work is enqueued (va_slots.hpp).
+struct Lease {
+    int dev = 0;
+    int slot = -1;
+    uintptr_t key = 0;
+    unsigned long long capture = 0;
+};
+
+// Ticket slot of a fused call on `stream` (va_slots.hpp: one per eager stream,
+// one per stream and capture sequence while capturing; an idle eager stream's
+// slot may be taken over), or slot -1: the call runs the two-pass form. The
+// per-thread default stream always runs the two-pass form.
+//
+// Stale tagged partials (va_kernels.hpp, TAG_EPOCH_BITS): every eager call is
+// counted against its slot, and after SLOT_CLEAR_CALLS of them the slot's
+// store is cleared on `stream` ahead of the call, so a word left by an eager
+// call is gone before any merge group's epoch has advanced 2^TAG_EPOCH_BITS
+// past it. Replays of a captured graph are not seen here: a capture's slot is
+// cleared when its binding is released (release_capture_all), before any
+// other owner can use it.
+Lease ticket_slot_for(void* stream) {
+    Lease l;
+    if (as_stream(stream) == hipStreamPerThread) return l;
+    if (hipGetDevice(&l.dev) != hipSuccess || !capture_of(stream, &l.capture)) return l;
+    l.key = owner_key(stream);
+    l.slot = g_slots.acquire(l.dev, l.key, l.capture, owner_idle);
+    if (l.slot >= 0 && l.capture == 0 && g_slots.count(l.dev, l.slot) >= va::SLOT_CLEAR_CALLS) {
+        if (clear_slot(l.slot, as_stream(stream)) != hipSuccess) {
+            g_slots.done(l.dev, l.slot, l.key, l.capture);
+            l.slot = -1;                          // two-pass form instead
+            return l;
+        }
+        g_slots.reset_count(l.dev, l.slot);
+    }
+    return l;
+}
+void lease_done(const Lease& l) {
+    if (l.slot >= 0) g_slots.done(l.dev, l.slot, l.key, l.capture);
+}
+
+// Drop (device, key, capture)'s ticket slot and workspace bindings once its
+// work is done, clearing the slot's tagged partials on `stream` (synchronised
+// here) so that its next owner starts from a clear store.
+hipError_t release_owner(int dev, uintptr_t key, unsigned long long capture, hipStream_t stream) {
+    hipError_t e = hipSuccess;
+    const int slot = g_slots.find(dev, key, capture);
+    if (slot >= 0) {
+        e = clear_slot(slot, stream);
+        if (e == hipSuccess) e = hipStreamSynchronize(stream);
+        g_slots.release(dev, key, capture);
+        g_slots.reset_count(dev, slot);
+    }
+    g_scratch_owner.release(dev, key, capture);
+    return e;
+}
+
+// Drop every binding of a capture sequence; the device has finished all work
+// (the caller synchronised it). The dropped slots are cleared on the null
+// stream and waited for.
+hipError_t release_capture_all(unsigned long long capture) {
+    if (capture == 0) return hipSuccess;
+    std::vector<std::pair<int, int>> dropped;
+    g_slots.release_capture(capture, [&](int d, int slot) { dropped.emplace_back(d, slot); });
+    g_scratch_owner.release_capture(capture);
+    int cur = 0;
+    hipError_t e = hipGetDevice(&cur);
+    for (const auto& x : dropped) {
+        if (e != hipSuccess) break;
+        e = hipSetDevice(x.first);
+        if (e == hipSuccess) e = clear_slot(x.second, nullptr);
+        if (e == hipSuccess) e = hipDeviceSynchronize();
+        g_slots.reset_count(x.first, x.second);
+    }
+    if (!dropped.empty()) (void)hipSetDevice(cur);
+    return e;
 }
 
 // slot >= 0: merge inside the decode kernel on that ticket slot (the caller
@@ -210,9 +320,10 @@ int va_decode(va_fmt fmt, const va_bufs* b, int H, int L, int D, int G, int S, v
     int rc = validate(fmt, b, H, L, D, G, S, true);
     if (rc) return rc;
     const bool fits = H <= va::TICKET_MAXH && S <= 64 && (long long)H * S <= va::PART_CAP;
-    const int slot = fits ? ticket_slot_for(stream) : -1;
-    rc = run_splits(fmt, b, H, L, D, G, S, stream, slot);
-    if (rc || slot >= 0) return rc;
+    const Lease lease = fits ? ticket_slot_for(stream) : Lease{};
+    rc = run_splits(fmt, b, H, L, D, G, S, stream, lease.slot);
+    lease_done(lease);
+    if (rc || lease.slot >= 0) return rc;
     const hipError_t e = va::launch_merge(b->ws, b->out, H, D, S, as_stream(stream));
     if (e != hipSuccess) return hip_fail(e, "merge launch");
     return VA_OK;
@@ -268,12 +379,30 @@ int va_decode_noalloc(va_fmt fmt, const va_bufs* b, int H, int L, int D, int G, 
     nb.ws = scratch_ptr(&rc);
     if (!nb.ws) return rc;
     const bool fits = H <= va::TICKET_MAXH && S <= 64 && (long long)H * S <= va::PART_CAP;
-    const int slot = fits ? ticket_slot_for(stream) : -1;
-    rc = run_splits(fmt, &nb, H, L, D, G, S, stream, slot);
-    if (rc || slot >= 0) return rc;
-    const hipError_t e = va::launch_merge(nb.ws, nb.out, H, D, S, as_stream(stream));
-    if (e != hipSuccess) return hip_fail(e, "merge launch");
-    return VA_OK;
+    const Lease lease = fits ? ticket_slot_for(stream) : Lease{};
+    if (lease.slot >= 0) {                       // fused merge: the workspace is not used
+        rc = run_splits(fmt, &nb, H, L, D, G, S, stream, lease.slot);
+        lease_done(lease);
+        return rc;
+    }
+    // Two-pass form: the device's workspace is bound to one owner (stream, or
+    // stream and capture sequence) at a time, taken over only from an idle
+    // eager stream with no call in progress; any other owner is refused.
+    Lease ws;
+    if (hipGetDevice(&ws.dev) != hipSuccess || !capture_of(stream, &ws.capture))
+        return fail(VA_EHIP, "cannot identify the calling stream");
+    ws.key = owner_key(stream);
+    ws.slot = g_scratch_owner.acquire(ws.dev, ws.key, ws.capture, owner_idle);
+    if (ws.slot < 0)
+        return fail(VA_EBUSY, "the allocation-free workspace of device %d is bound to another stream or graph "
+                              "(va_stream_release / va_capture_release free it)", ws.dev);
+    rc = run_splits(fmt, &nb, H, L, D, G, S, stream, -1);
+    if (rc == VA_OK) {
+        const hipError_t e = va::launch_merge(nb.ws, nb.out, H, D, S, as_stream(stream));
+        if (e != hipSuccess) rc = hip_fail(e, "merge launch");
+    }
+    g_scratch_owner.done(ws.dev, ws.slot, ws.key, ws.capture);
+    return rc;
 }
 
 int va_decode_splits(va_fmt fmt, const va_bufs* b, int H, int L, int D, int G, int S, void* stream) {
@@ -359,11 +488,13 @@ bool fused_ok(int groups, int qg, int S) {
 
 int launch_ex(va_fmt fmt, va::DecodeArgs& a, int D, int G, int qg, bool paged, int groups,
               int heads_total, void* stream) {
-    a.ticket_slot = fused_ok(groups, qg, a.S) ? ticket_slot_for(stream) : -1;
+    const Lease lease = fused_ok(groups, qg, a.S) ? ticket_slot_for(stream) : Lease{};
+    a.ticket_slot = lease.slot;
     const bool fused = a.ticket_slot >= 0;
     a.qscale = (float)(1.4426950408889634074 / std::sqrt((double)D));
     hipError_t e = va::launch_decode_ex(kind_of(fmt), D, is_f16(fmt) ? 64 : G, qg, paged, groups, a,
                                         as_stream(stream));
+    lease_done(lease);
     if (e != hipSuccess) return hip_fail(e, "decode launch");
     if (!fused) {
         e = va::launch_merge(a.ws, a.out, heads_total, D, a.S, as_stream(stream));
@@ -880,12 +1011,24 @@ int va_stream_create(void** stream) {
     return VA_OK;
 }
 int va_stream_destroy(void* stream) {
-    // The stream's ticket slot is freed once its last call has finished.
+    // The stream's bindings are freed once its last call has finished.
     VA_HIP(hipStreamSynchronize(as_stream(stream)), "hipStreamSynchronize");
     int dev = 0;
     VA_HIP(hipGetDevice(&dev), "hipGetDevice");
-    g_slots.release(dev, reinterpret_cast<uintptr_t>(stream), 0);
+    VA_HIP(release_owner(dev, owner_key(stream), 0, as_stream(stream)), "release stream bindings");
     VA_HIP(hipStreamDestroy(as_stream(stream)), "hipStreamDestroy");
+    return VA_OK;
+}
+int va_stream_release(void* stream) {
+    VA_HIP(hipStreamSynchronize(as_stream(stream)), "hipStreamSynchronize");
+    int dev = 0;
+    VA_HIP(hipGetDevice(&dev), "hipGetDevice");
+    VA_HIP(release_owner(dev, owner_key(stream), 0, as_stream(stream)), "release stream bindings");
+    return VA_OK;
+}
+int va_capture_release(unsigned long long capture_id) {
+    VA_HIP(hipDeviceSynchronize(), "hipDeviceSynchronize");
+    VA_HIP(release_capture_all(capture_id | (1ull << 63)), "release capture bindings");
     return VA_OK;
 }
 int va_stream_sync(void* stream) {
@@ -933,14 +1076,14 @@ int va_graph_end(void* stream, void** graph_exec) {
     hipGraph_t g = nullptr;
     hipError_t e = hipStreamEndCapture(as_stream(stream), &g);
     if (e != hipSuccess) {                       // no graph: nothing can replay the capture's slots
-        g_slots.release_capture(capture);
+        (void)release_capture_all(capture);
         return hip_fail(e, "hipStreamEndCapture");
     }
     hipGraphExec_t x = nullptr;
     e = hipGraphInstantiate(&x, g, nullptr, nullptr, 0);
     (void)hipGraphDestroy(g);
     if (e != hipSuccess) {
-        g_slots.release_capture(capture);
+        (void)release_capture_all(capture);
         return hip_fail(e, "hipGraphInstantiate");
     }
     if (capture) {
@@ -967,7 +1110,7 @@ int va_graph_destroy(void* graph_exec) {
     }
     if (capture) VA_HIP(hipDeviceSynchronize(), "hipDeviceSynchronize");
     VA_HIP(hipGraphExecDestroy(static_cast<hipGraphExec_t>(graph_exec)), "hipGraphExecDestroy");
-    g_slots.release_capture(capture);
+    VA_HIP(release_capture_all(capture), "release capture bindings");
     return VA_OK;
 }
 

@@ -29,7 +29,7 @@ from typing import Optional
 
 import torch
 
-from . import (Fmt, _Bufs, _PagedBufs, _PagedShape, check, fmt_bits, lib, row_bytes, ws_bytes)
+from . import (Fmt, _Bufs, _PagedBufs, _PagedShape, check, fmt_bits, lib, ws_bytes)
 
 __all__ = ["decode", "decode_gqa", "decode_paged", "append_kv", "quantize", "dequantize"]
 
@@ -62,31 +62,45 @@ def _fail(msg: str):
     raise RuntimeError(f"voltattn: {msg}")
 
 
+# The validators run in the real and the fake (meta) implementations alike.
+# Sizes may be symbolic (torch.compile with dynamic shapes): they are compared
+# with torch._check, which records a runtime assertion instead of fixing a
+# size to its traced value, and are never converted with int() here, so a
+# decode loop whose L grows does not recompile on every step. Only the head
+# dimension D (64 or 128) and the group size decide which kernel runs.
+
+def _check(cond, msg) -> None:
+    torch._check(cond, lambda: f"voltattn: {msg()}")
+
+
 def _expect(t: torch.Tensor, name: str, shape: tuple, dtype: torch.dtype) -> None:
     if t is None:
         _fail(f"{name} is required")
-    if tuple(int(x) for x in t.shape) != tuple(shape):
+    if t.dim() != len(shape):
         _fail(f"{name} has shape {tuple(t.shape)}, expected {tuple(shape)}")
+    for got, want in zip(t.shape, shape):
+        _check(got == want, lambda: f"{name} has shape {tuple(t.shape)}, expected {tuple(shape)}")
     if t.dtype != dtype:
         _fail(f"{name} has dtype {t.dtype}, expected {dtype}")
 
 
-def _check_dg(f: Fmt, D: int, group: int) -> None:
-    if D not in (64, 128):
-        _fail(f"D must be 64 or 128 (got {D})")
-    if fmt_bits(f) != 16 and not (group in (32, 64) and group <= D):
-        _fail(f"group must be 32 or 64 and <= D (got {group}, D={D})")
+def _check_dg(f: Fmt, D, group: int) -> None:
+    _check((D == 64) | (D == 128), lambda: f"D must be 64 or 128 (got {D})")
+    if fmt_bits(f) != 16:
+        if group not in (32, 64):
+            _fail(f"group must be 32 or 64 (got {group})")
+        _check(D >= group, lambda: f"group must be <= D (got {group}, D={D})")
 
 
-def _row_shape(f: Fmt, D: int) -> tuple[tuple, torch.dtype]:
+def _row_shape(f: Fmt, D) -> tuple[tuple, torch.dtype]:
     """Trailing shape and dtype of one K/V row of format f: fp16 [D] for the f16
     formats, uint8 [row bytes] for the quantized ones."""
     if fmt_bits(f) == 16:
         return (D,), torch.float16
-    return (row_bytes(f, D),), torch.uint8
+    return (D * fmt_bits(f) // 8,), torch.uint8
 
 
-def _check_kv(f: Fmt, k, v, ks, vs, lead: tuple, D: int, group: int) -> None:
+def _check_kv(f: Fmt, k, v, ks, vs, lead: tuple, D, group: int) -> None:
     """k, v [*lead, row]; scales fp16 [*lead, D/G] for quantized formats."""
     tail, dt = _row_shape(f, D)
     _expect(k, "k", lead + tail, dt)
@@ -99,57 +113,58 @@ def _check_kv(f: Fmt, k, v, ks, vs, lead: tuple, D: int, group: int) -> None:
 def _validate_decode(q, k, v, ks, vs, f: Fmt, group: int, grouped: bool) -> None:
     if q.dim() != 2:
         _fail(f"q must be [H, D] (got {tuple(q.shape)})")
-    H, D = (int(x) for x in q.shape)
+    H, D = q.shape
     _expect(q, "q", (H, D), torch.float16)
     _check_dg(f, D, group)
     if k.dim() != 3:
         _fail(f"k must be [heads, L, row] (got {tuple(k.shape)})")
-    Hk, L = int(k.shape[0]), int(k.shape[1])
+    Hk, L = k.shape[0], k.shape[1]
     if grouped:
-        if Hk < 1 or H % Hk:
-            _fail(f"query heads ({H}) must be a multiple of K/V heads ({Hk})")
-    elif Hk != H:
-        _fail(f"k has {Hk} heads, q has {H}")
+        _check(Hk >= 1, lambda: f"k must have at least one head (got {Hk})")
+        _check(H % Hk == 0, lambda: f"query heads ({H}) must be a multiple of K/V heads ({Hk})")
+    else:
+        _check(Hk == H, lambda: f"k has {Hk} heads, q has {H}")
     _check_kv(f, k, v, ks, vs, (Hk, L), D, group)
 
 
 def _validate_paged(q, kp, vp, ksp, vsp, block_table, seq_lens, f: Fmt, group: int) -> None:
     if q.dim() != 3:
         _fail(f"q must be [B, Hq, D] (got {tuple(q.shape)})")
-    B, Hq, D = (int(x) for x in q.shape)
+    B, Hq, D = q.shape
     _expect(q, "q", (B, Hq, D), torch.float16)
     _check_dg(f, D, group)
     if kp.dim() != 4:
         _fail(f"k_pages must be [num_pages, Hkv, page_rows, row] (got {tuple(kp.shape)})")
-    num_pages, Hkv, page_rows = (int(x) for x in kp.shape[:3])
-    if Hkv < 1 or Hq % Hkv:
-        _fail(f"query heads ({Hq}) must be a multiple of K/V heads ({Hkv})")
+    num_pages, Hkv, page_rows = kp.shape[:3]
+    _check(Hkv >= 1, lambda: f"k_pages must have at least one head (got {Hkv})")
+    _check(Hq % Hkv == 0, lambda: f"query heads ({Hq}) must be a multiple of K/V heads ({Hkv})")
     _check_kv(f, kp, vp, ksp, vsp, (num_pages, Hkv, page_rows), D, group)
-    if block_table.dim() != 2 or int(block_table.shape[0]) != B:
+    if block_table.dim() != 2:
         _fail(f"block_table must be [B={B}, max_pages] (got {tuple(block_table.shape)})")
-    _expect(block_table, "block_table", (B, int(block_table.shape[1])), torch.int32)
+    _check(block_table.shape[0] == B, lambda: f"block_table must be [B={B}, max_pages] (got {tuple(block_table.shape)})")
+    _expect(block_table, "block_table", (B, block_table.shape[1]), torch.int32)
     _expect(seq_lens, "seq_lens", (B,), torch.int32)
 
 
 def _validate_append(x, start, block_table, pages, scale_pages, f: Fmt, group: int) -> None:
     if x.dim() != 4:
         _fail(f"x must be [B, Hkv, n, D] (got {tuple(x.shape)})")
-    B, Hkv, n, D = (int(s) for s in x.shape)
+    B, Hkv, n, D = x.shape
     _expect(x, "x", (B, Hkv, n, D), torch.float16)
     _check_dg(f, D, group)
     if pages.dim() != 4:
         _fail(f"pages must be [num_pages, Hkv, page_rows, row] (got {tuple(pages.shape)})")
-    num_pages, Hp, page_rows = (int(s) for s in pages.shape[:3])
-    if Hp != Hkv:
-        _fail(f"pages hold {Hp} K/V heads, x has {Hkv}")
+    num_pages, Hp, page_rows = pages.shape[:3]
+    _check(Hp == Hkv, lambda: f"pages hold {Hp} K/V heads, x has {Hkv}")
     tail, dt = _row_shape(f, D)
     _expect(pages, "pages", (num_pages, Hkv, page_rows) + tail, dt)
     if fmt_bits(f) != 16:
         _expect(scale_pages, "scale_pages", (num_pages, Hkv, page_rows, D // group), torch.float16)
     _expect(start, "start", (B,), torch.int32)
-    if block_table.dim() != 2 or int(block_table.shape[0]) != B:
+    if block_table.dim() != 2:
         _fail(f"block_table must be [B={B}, max_pages] (got {tuple(block_table.shape)})")
-    _expect(block_table, "block_table", (B, int(block_table.shape[1])), torch.int32)
+    _check(block_table.shape[0] == B, lambda: f"block_table must be [B={B}, max_pages] (got {tuple(block_table.shape)})")
+    _expect(block_table, "block_table", (B, block_table.shape[1]), torch.int32)
 
 
 def _validate_quantize(x, bits: int, group: int) -> None:
@@ -157,23 +172,30 @@ def _validate_quantize(x, bits: int, group: int) -> None:
         _fail(f"bits must be 8, 4 or 3 (got {bits})")
     if x.dtype != torch.float32:
         _fail(f"x must be fp32 (got {x.dtype})")
-    D = int(x.shape[-1]) if x.dim() else 0
-    if not (group in (32, 64) and D >= group and D % group == 0 and D % 8 == 0):
-        _fail(f"group must be 32 or 64 and divide D (got group={group}, D={D})")
+    if group not in (32, 64):
+        _fail(f"group must be 32 or 64 (got {group})")
+    if x.dim() == 0:
+        _fail("x must have a last dimension D")
+    D = x.shape[-1]
+    _check((D >= group) & (D % group == 0) & (D % 8 == 0),
+           lambda: f"group must be 32 or 64 and divide D (got group={group}, D={D})")
 
 
-def _validate_dequantize(packed, scales, bits: int, group: int) -> int:
+def _validate_dequantize(packed, scales, bits: int, group: int):
     """Checks packed uint8 [..., D*bits/8] and scales fp16 [..., D/G]; returns D."""
     if bits not in (8, 4, 3):
         _fail(f"bits must be 8, 4 or 3 (got {bits})")
     if packed.dtype != torch.uint8:
         _fail(f"packed must be uint8 (got {packed.dtype})")
-    nb = int(packed.shape[-1]) if packed.dim() else 0
-    if nb * 8 % bits:
-        _fail(f"packed rows of {nb} bytes do not hold whole {bits}-bit codes")
+    if group not in (32, 64):
+        _fail(f"group must be 32 or 64 (got {group})")
+    if packed.dim() == 0:
+        _fail("packed must have a last dimension (row bytes)")
+    nb = packed.shape[-1]
+    _check(nb * 8 % bits == 0, lambda: f"packed rows of {nb} bytes do not hold whole {bits}-bit codes")
     D = nb * 8 // bits
-    if not (group in (32, 64) and D >= group and D % group == 0 and D % 8 == 0):
-        _fail(f"group must be 32 or 64 and divide D (got group={group}, D={D})")
+    _check((D >= group) & (D % group == 0) & (D % 8 == 0),
+           lambda: f"group must be 32 or 64 and divide D (got group={group}, D={D})")
     _expect(scales, "scales", tuple(packed.shape[:-1]) + (D // group,), torch.float16)
     return D
 
@@ -314,7 +336,7 @@ def _(x, bits, group=32):
 @torch.library.custom_op("voltattn::dequantize", mutates_args=())
 def dequantize(packed: torch.Tensor, scales: torch.Tensor, bits: int, group: int = 32) -> torch.Tensor:
     """(packed uint8 [..., D*bits/8], fp16 scales [..., D/G]) -> fp32 [..., D], bit-exact dq()."""
-    D = _validate_dequantize(packed, scales, bits, group)
+    D = int(_validate_dequantize(packed, scales, bits, group))
     _need_gpu(packed, scales)
     rows = packed.numel() // max(1, int(packed.shape[-1]))
     out = torch.empty(packed.shape[:-1] + (D,), dtype=torch.float32, device=packed.device)
