@@ -144,17 +144,12 @@ def test_graph_capture_needs_a_stream():
 
 def test_pick_splits_rule():
     """The split rule on 256 CUs (the MI355X count, and the default without a device):
-    one work-group per CU at H=32 (S=8), except q3 rows, which take two per CU once
-    every split still spans >= 4096 positions (their VALU-bound loop hides more
-    latency at four waves per SIMD)."""
-    for f in (va.Fmt.F16M, va.Fmt.Q8M, va.Fmt.Q4M):
+    one work-group per CU, so S = 256 / H (S=8 at H=32, 32 at H=8), every format."""
+    for f in (va.Fmt.F16M, va.Fmt.Q8M, va.Fmt.Q4M, va.Fmt.Q3M):
         for L in (4096, 16384, 65536, 262144):
             assert va.pick_splits(f, 32, L, 128) == 8, (f.label, L)
-    for L, S in ((4096, 8), (16384, 8), (32768, 8), (65536, 16), (131072, 16), (262144, 16)):
-        assert va.pick_splits(va.Fmt.Q3M, 32, L, 128) == S, L
-        assert va.split_chunk(L, S) >= 4096 or S == 8
     assert va.pick_splits(va.Fmt.Q3M, 8, 65536, 128) == 32
-    assert va.pick_splits(va.Fmt.Q3M, 8, 262144, 128) == 64
+    assert va.pick_splits(va.Fmt.Q3M, 8, 262144, 128) == 32
 
 
 def test_probe_argument_checks():

@@ -136,7 +136,7 @@ __global__ __launch_bounds__(256) void decode_w1(DecodeArgs a) {
 #define VA_Q4_DEEP 1
 #endif
 #ifndef VA_Q3_WAVES
-#define VA_Q3_WAVES 8                // 8 waves x 2 rows (128 VGPRs: two waves per SIMD)
+#define VA_Q3_WAVES 8                // 8 waves x 2 rows
 #endif
 #ifndef VA_Q3_DEEP
 #define VA_Q3_DEEP 0
@@ -144,9 +144,9 @@ __global__ __launch_bounds__(256) void decode_w1(DecodeArgs a) {
 
 template <int KIND> struct TiledCfg;
 template <> struct TiledCfg<KF16> { static constexpr int waves = VA_F16_WAVES; static constexpr bool deep = VA_F16_DEEP; };
-template <> struct TiledCfg<KQ8>  { static constexpr int waves = VA_Q8_WAVES;  static constexpr bool deep = VA_Q8_DEEP; };
-template <> struct TiledCfg<KQ4>  { static constexpr int waves = VA_Q4_WAVES;  static constexpr bool deep = VA_Q4_DEEP; };
-template <> struct TiledCfg<KQ3>  { static constexpr int waves = VA_Q3_WAVES;  static constexpr bool deep = VA_Q3_DEEP; };
+template <> struct TiledCfg<KQ8>  { static constexpr int waves = VA_Q8_WAVES;  static constexpr bool deep = VA_Q8_DEEP;  };
+template <> struct TiledCfg<KQ4>  { static constexpr int waves = VA_Q4_WAVES;  static constexpr bool deep = VA_Q4_DEEP;  };
+template <> struct TiledCfg<KQ3>  { static constexpr int waves = VA_Q3_WAVES;  static constexpr bool deep = VA_Q3_DEEP;  };
 template <int KIND> struct TiledShape {
     static_assert(TiledCfg<KIND>::waves == 4 || TiledCfg<KIND>::waves == 8, "4 or 8 waves per group");
     static constexpr int waves = TiledCfg<KIND>::waves;

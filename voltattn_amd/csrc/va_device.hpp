@@ -115,10 +115,15 @@ constexpr int DPP_ROW_HALF_MIRROR = 0x141;
 constexpr int DPP_ROW_MIRROR = 0x140;
 constexpr int dpp_row_ror(int n) { return 0x120 + n; }   // n in 1..15
 
+// All rows and banks enabled; bound_ctrl set, so a lane whose source is out
+// of range reads 0 (the "old" operand is 0 as well, so the result is the same
+// either way). With bound_ctrl set the compiler folds the move into the
+// consuming add/max as one DPP instruction instead of a v_mov_b32_dpp plus a
+// v_mov_b32 of the old value.
 template <int CTRL>
 __device__ __forceinline__ float dpp(float x) {
     return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x),
-                                                                 CTRL, 0xF, 0xF, false));
+                                                                 CTRL, 0xF, 0xF, true));
 }
 
 // Sum over aligned groups of N consecutive lanes (N in 1,2,4,8,16); every lane
@@ -178,6 +183,18 @@ __device__ __forceinline__ float rows_max(float x) {
     b = a;
     permlane32_swap(a, b);
     return fmaxf(__builtin_bit_cast(float, a), __builtin_bit_cast(float, b));
+}
+
+// Max over aligned groups of N consecutive lanes (N in 1,2,4,8,16), in every
+// lane of the group; same butterfly as group_sum.
+template <int N>
+__device__ __forceinline__ float group_max(float x) {
+    static_assert(N == 1 || N == 2 || N == 4 || N == 8 || N == 16, "group size");
+    if constexpr (N >= 2)  x = fmaxf(x, dpp<DPP_QP_XOR1>(x));
+    if constexpr (N >= 4)  x = fmaxf(x, dpp<DPP_QP_XOR2>(x));
+    if constexpr (N >= 8)  x = fmaxf(x, dpp<DPP_ROW_HALF_MIRROR>(x));
+    if constexpr (N >= 16) x = fmaxf(x, dpp<DPP_ROW_MIRROR>(x));
+    return x;
 }
 
 // Full-wave max and sum (all 64 lanes receive the result).

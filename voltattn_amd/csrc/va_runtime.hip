@@ -303,12 +303,10 @@ int va_pick_splits(va_fmt fmt, int H, int L, int D, int* S) {
     // stream a CU at full rate; more splits only lengthen the merge). Naive
     // kernels keep one position per wave in flight, so they need ~8 per CU.
     int per_cu = va::groups_per_cu(kind_of(fmt), tiled_of(fmt));
-    // q3 rows are VALU-bound on long splits: a second work-group per CU (four
-    // waves per SIMD) hides more of the dependent-op latency once every split
-    // still spans >= 4096 positions. Measured on MI355X (H=32, D=128, S 8 -> 16):
-    // L=65536 -1%, 131072 -2.5%, 262144 -2%; L=16384-32768 +1.5%, so shorter
-    // contexts keep one group per CU.
-    if (fmt == VA_Q3P && (long long)L * H >= 4096LL * 2 * per_cu * cus) per_cu *= 2;
+    // (q3 once took a second work-group per CU on long contexts, while its
+    // kernel fit four waves per SIMD. The kernel now holds ~150 VGPRs, one
+    // group per CU, and one split per CU measured faster on MI355X (H=32,
+    // D=128): L=65536 46.2 -> 42.4 us, L=262144 157.6 -> 156.2 us.)
     const int target = std::max(1, (per_cu * cus + H - 1) / H);
     const int s0     = std::max(1, std::min(tiles, target));
     const int tps    = (tiles + s0 - 1) / s0;               // tiles per split

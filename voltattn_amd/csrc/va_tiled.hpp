@@ -8,10 +8,11 @@
 // src/voltattn.cu:80-120, 364-649, which has QG = 1 and contiguous K/V).
 // Each lane takes LB = 16 contiguous bytes (12 for q3) of a row with one
 // buffer load, so one wave-wide load instruction covers PPW = 64/LP rows with
-// no gaps; each row is unpacked once into exact fp16 pairs (va_codec.hpp) and
-// used by all QG query heads, the partial dot is summed over the LP lanes with
-// DPP row ops, and the online softmax runs in fp32 in log2 units (q is
-// pre-scaled by log2(e)/sqrt(D), exponentials are v_exp_f32). Per wave and
+// no gaps; each row is unpacked once into fp16 pairs (va_codec.hpp) and used
+// by all QG query heads, the partial dot is summed over the LP lanes with DPP
+// row ops, and the online softmax runs in fp32 in log2 units: scores stay raw
+// (q.k times the group scale) and qs = log2(e)/sqrt(D) enters through the
+// exponent's fma, exp2(score * qs - m) on v_exp_f32. Per wave and
 // iteration U rows per lane are in flight for K and V, and the next tile is
 // prefetched into registers while the current one is computed. The fp16 group
 // scales of a wave's tile are fetched with one coalesced load per tensor and
@@ -41,6 +42,8 @@
 #pragma once
 #include "va_codec.hpp"
 #include "va_fused.hpp"
+
+#include <type_traits>
 
 namespace va {
 
@@ -221,7 +224,7 @@ __global__ __launch_bounds__(WAVES * 64, MINB) void decode_tiled(
         typename C::QReg qr[QG];
 #pragma unroll
         for (int q = 0; q < QG; ++q)
-            C::load_q(qr[q], a.q + (size_t)(rt.oh0 + (q < rt.nq ? q : 0)) * D + sl * EPL, a.qscale);
+            C::template load_q<LP>(qr[q], a.q + (size_t)(rt.oh0 + (q < rt.nq ? q : 0)) * D + sl * EPL, a.qscale);
         const uint32_t magic = C::magic();
 
         auto stage_scales = [&](const uint32_t* sk, const uint32_t* sv) {  // (k | v << 16) pairs
@@ -241,38 +244,68 @@ __global__ __launch_bounds__(WAVES * 64, MINB) void decode_tiled(
             }
         };
 
-        auto compute_tile = [&](int it, const LoadT* kk, const LoadT* vv) {
-            const int rem = uniform(n - it * TB - wave * TW);   // valid rows of this wave tile
+        // V offset window: S[q] sums the weights ev since the last fix_v, which
+        // removes the stored codes' offset from the accumulators in bulk once
+        // per tile pair (2U rows per lane), so the sums never drift more than a
+        // pair's worth from the signed ones. (An fp32 emulation of the
+        // accumulation error against the exact sum: the same as signed
+        // accumulation for windows up to 32 rows, q8 / q4 / q3 alike. Fixing
+        // every other pair instead measured slower on MI355X: the conditional
+        // splits the loop body.)
+        float S[QG];
+#pragma unroll
+        for (int q = 0; q < QG; ++q) S[q] = 0.f;
+        auto fix_v = [&]() {
+            if constexpr (C::VFIX) {
+#pragma unroll
+                for (int q = 0; q < QG; ++q) {
+#pragma unroll
+                    for (int e = 0; e < EPL; ++e) o[q][e] = __builtin_fmaf(S[q], C::voff(e), o[q][e]);
+                    S[q] = 0.f;
+                }
+            }
+        };
+
+        // Scores stay raw (q.k times the group scale); qs is applied inside the
+        // exponent's fma and to the tile maximum.
+        auto compute_tile = [&](auto masked, int it, const LoadT* kk, const LoadT* vv) {
+            constexpr bool MASK = decltype(masked)::value;
             float sc[QG][U];
             uint32_t pair[U];
 #pragma unroll
             for (int u = 0; u < U; ++u) {
                 const int slot = u * PPW + pw;
                 h2 pk[NP];
-                C::unpack(kk[u], magic, pk);
-                float ks = 1.f;
+                C::unpack_k(kk[u], magic, pk);
                 pair[u] = 0;
-                if constexpr (QUANT) {
-                    pair[u] = s_scale[wave][slot * NG + grp];
-                    ks = h2f_lo(pair[u]);
-                }
+                if constexpr (QUANT) pair[u] = s_scale[wave][slot * NG + grp];
 #pragma unroll
                 for (int q = 0; q < QG; ++q) {
                     float d = C::dot(pk, qr[q]);
-                    if constexpr (QUANT) d *= ks;
-                    d = group_sum<LP>(d);
-                    sc[q][u] = slot < rem ? d : -__builtin_inff();
+                    if constexpr (QUANT) d = mul_lo_h(d, pair[u]);     // x k scale
+                    sc[q][u] = group_sum<LP>(d);
                 }
+            }
+            // Rows past the split end score -inf (the masked form of the loop).
+            if constexpr (MASK) {
+                const int rem = uniform(n - it * TB - wave * TW);   // valid rows of this wave tile
+#pragma unroll
+                for (int u = 0; u < U; ++u)
+#pragma unroll
+                    for (int q = 0; q < QG; ++q)
+                        sc[q][u] = u * PPW + pw < rem ? sc[q][u] : -__builtin_inff();
             }
 #pragma unroll
             for (int q = 0; q < QG; ++q) {
                 float tmax = sc[q][0];
 #pragma unroll
                 for (int u = 1; u < U; ++u) tmax = fmaxf(tmax, sc[q][u]);
+                tmax *= qr[q].qs;                                      // log2 units
                 if (__builtin_amdgcn_ballot_w64(tmax > m[q] + RESCALE_SLACK)) {
                     const float mn = uniformf(wave_max(fmaxf(m[q], tmax)));
                     const float c  = fast_exp2(m[q] - mn);
                     l[q] *= c;
+                    S[q] *= c;
 #pragma unroll
                     for (int e = 0; e < EPL; ++e) o[q][e] *= c;
                     m[q] = mn;
@@ -281,14 +314,15 @@ __global__ __launch_bounds__(WAVES * 64, MINB) void decode_tiled(
 #pragma unroll
             for (int u = 0; u < U; ++u) {
                 h2 pv[NP];
-                C::unpack(vv[u], magic, pv);
+                C::unpack_v(vv[u], pv);
 #pragma unroll
                 for (int q = 0; q < QG; ++q) {
-                    const float p = fast_exp2(sc[q][u] - m[q]);
+                    const float p = fast_exp2(__builtin_fmaf(sc[q][u], qr[q].qs, -m[q]));
                     l[q] += p;
                     float ev = p;
-                    if constexpr (QUANT) ev = p * h2f_hi(pair[u]);
-                    C::axpy(pv, ev, o[q]);
+                    if constexpr (QUANT) ev = mul_hi_h(p, pair[u]);    // x v scale
+                    if constexpr (C::VFIX) S[q] += ev;
+                    C::axpy_v(pv, ev, o[q]);
                 }
             }
         };
@@ -301,27 +335,40 @@ __global__ __launch_bounds__(WAVES * 64, MINB) void decode_tiled(
         // one-slot form, and skipping the last prefetch with a uniform test made
         // q4+ at H=32 L=16384 1.7 us slower: both change how the loop body is
         // scheduled.)
-        const int npair = niter / 2;
         // f16 rows in 8-wave groups: the older wave of each SIMD pair wins issue
         // and runs ahead, and the younger one finishes alone with half the loads
         // in flight. On long splits a barrier per tile pair keeps the waves
         // together (measured on MI355X, H=32 D=128: L=65536 165.7 -> 161.3 us);
         // below 16 tiles per group it costs more than it saves (L=4096 +0.35 us).
         const bool lockstep = KIND == KF16 && WAVES == 8 && QG == 1 && !PAGED && niter >= 16;
-        for (int ip = 0; ip < npair; ++ip) {
+        // Only the last work-group tile of a split can hold rows past its end
+        // (rem < TW for some wave), so only that tile runs the masked form; the
+        // pair loop covers tiles 0 .. 2P-1, all full.
+        const int P = (niter - 1) / 2;
+        for (int ip = 0; ip < P; ++ip) {
             const int it = 2 * ip;
             if (lockstep) __builtin_amdgcn_s_barrier();     // niter is uniform over the group
             stage_scales(ska, sva);
             load_tile(it + 1, kb, vb, skb, svb);
-            compute_tile(it, ka, va_);
+            compute_tile(std::false_type{}, it, ka, va_);
             stage_scales(skb, svb);
             load_tile(it + 2, ka, va_, ska, sva);
-            compute_tile(it + 1, kb, vb);
+            compute_tile(std::false_type{}, it + 1, kb, vb);
+            fix_v();
         }
-        if (niter & 1) {
+        // tail: tile 2P is in the A stage; it is the last one, or one full tile
+        // and then the last
+        if (niter - 2 * P == 2) {
             stage_scales(ska, sva);
-            compute_tile(niter - 1, ka, va_);
+            load_tile(2 * P + 1, kb, vb, skb, svb);
+            compute_tile(std::false_type{}, 2 * P, ka, va_);
+            stage_scales(skb, svb);
+            compute_tile(std::true_type{}, 2 * P + 1, kb, vb);
+        } else {
+            stage_scales(ska, sva);
+            compute_tile(std::true_type{}, 2 * P, ka, va_);
         }
+        fix_v();
 #pragma unroll
         for (int q = 0; q < QG; ++q) C::finish(o[q]);
     }
