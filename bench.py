@@ -22,6 +22,8 @@ Method (reference bench, src/voltattn.cu:967-1070, re-derived for MI355X):
   * K/V are drawn N(0,1) on the GPU, quantized there (bit-exact quantizer) and
     replicated into enough copies to rotate a >= 2 GiB working set, so the
     MALL cannot serve the stream;
+  * warm-up: untimed steps for >= 50 ms of wall time per row (--warm-ms), so
+    the shader clock has ramped from its idle level, then W warm-up steps;
   * timed region: device synchronisation, one untimed lead step (so the start
     event is stamped while the GPU is busy and the host's latency to enqueue
     the first timed step is not counted), then K back-to-back steps between two
@@ -145,7 +147,8 @@ class Workload:
         self.bufs = []
 
 
-def time_workload(va, w: Workload, steps: int, warmup: int, stream, steps_only: bool = False) -> dict:
+def time_workload(va, w: Workload, steps: int, warmup: int, stream, steps_only: bool = False,
+                  warm_ms: float = 50.0) -> dict:
     H, L, D, G, S, fmt = w.H, w.L, w.D, w.G, w.S, w.fmt
     bufs = [w.bufs_for(c) for c in range(w.copies)]
     launch = lambda c: va.launch(fmt, bufs[c % w.copies], H, L, D, S, G=G, stream=stream)
@@ -159,6 +162,17 @@ def time_workload(va, w: Workload, steps: int, warmup: int, stream, steps_only: 
         # is >= 2 GiB against a 256 MB MALL.
         for c in range(w.copies):
             launch(c)
+        # Clock warm-up: untimed steps for >= warm_ms of wall time, so the
+        # shader clock has left its idle level (MI355X idles near 100 MHz and
+        # ramps over tens of ms; a VALU-bound row timed cold measured 25-30 %
+        # slower), then the W warm-up steps.
+        t_end = time.perf_counter() + warm_ms / 1e3
+        i = 0
+        while time.perf_counter() < t_end:
+            launch(i)
+            i += 1
+            if i % 32 == 0:
+                va.sync()
         for i in range(warmup):
             launch(i)
         va.sync()
@@ -238,6 +252,13 @@ def time_fn(va, fn, copies: int, steps: int, warmup: int, stream) -> float:
     try:
         for c in range(copies):
             fn(c, stream)
+        t_end = time.perf_counter() + 0.05  # clock warm-up, as in time_workload
+        i = 0
+        while time.perf_counter() < t_end:
+            fn(i % copies, stream)
+            i += 1
+            if i % 32 == 0:
+                va.sync()
         for i in range(warmup):
             fn(i % copies, stream)
         va.sync()
@@ -426,8 +447,11 @@ CONFIG_ROWS = [
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=3)
+    # 100 steps keep the timed region of the longest row under 20 ms while the
+    # mean stops moving with the launch count (20 steps read 0.5-1 us higher on
+    # the 16K rows than 40-100 back to back).
+    ap.add_argument("--steps", type=int, default=100)
+    ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--G", type=int, default=32)
     ap.add_argument("--H", type=int, default=32)
     ap.add_argument("--D", type=int, default=128)
@@ -436,6 +460,8 @@ def main() -> int:
     ap.add_argument("--rows", default="all",
                     help="'all' (every BASELINE config) or a comma list of fmt:L, e.g. q8+:16384,f16+:16384")
     ap.add_argument("--splits", type=int, default=0, help="force S (0: va_pick_splits)")
+    ap.add_argument("--warm-ms", type=float, default=50.0,
+                    help="untimed steps for at least this long before each row's timed region")
     ap.add_argument("--probe-gib", type=float, default=4.0)
     ap.add_argument("--set-gib", type=float, default=2.0, help="rotated working set per row")
     ap.add_argument("--no-cpu", action="store_true")
@@ -496,7 +522,7 @@ def main() -> int:
         try:
             S = args.splits or va.pick_splits(fmt, H, L, D)
             w.set_splits(S)
-            t = time_workload(va, w, args.steps, args.warmup, stream, args.steps_only)
+            t = time_workload(va, w, args.steps, args.warmup, stream, args.steps_only, args.warm_ms)
             chk = {"checked": None} if args.no_check else check_workload(va, w, (0, H // 2, H - 1))
         finally:
             w.free()

@@ -299,11 +299,20 @@ __device__ constexpr int q3_shift(int e) {          // r of element e in its pai
 template <> struct Codec<KQ3> {
     static constexpr int EPL = 32, NP = 16;
     struct QReg { h2 q[NP]; float qs; };     // q[i] = (q_a 2^(k - r), q_b 2^(k - r')) of pair i
+    // The funnel shifts are asm so that both pairs of a window share one
+    // instruction: with the builtin, the compiler narrows a pair whose masked
+    // bits all come from one dword to a separate shift (one extra op per
+    // window, measured in the q3 loop).
+    __device__ static uint32_t funnel(uint32_t hi, uint32_t lo, int s) {
+        uint32_t r;
+        asm("v_alignbit_b32 %0, %1, %2, %3" : "=v"(r) : "v"(hi), "v"(lo), "i"(s));
+        return r;
+    }
     __device__ static uint32_t window(const u32x3& w, int s) {
         if (s == 0) return w.x;
-        if (s < 32) return __builtin_amdgcn_alignbit(w.y, w.x, s);
+        if (s < 32) return funnel(w.y, w.x, s);
         if (s == 32) return w.y;
-        if (s < 64) return __builtin_amdgcn_alignbit(w.z, w.y, s - 32);
+        if (s < 64) return funnel(w.z, w.y, s - 32);
         return w.z >> (s - 64);
     }
     template <int I>

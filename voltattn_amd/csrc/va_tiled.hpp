@@ -252,9 +252,12 @@ __global__ __launch_bounds__(WAVES * 64, MINB) void decode_tiled(
         // accumulation for windows up to 32 rows, q8 / q4 / q3 alike. Fixing
         // every other pair instead measured slower on MI355X: the conditional
         // splits the loop body.)
-        float S[QG];
+        float S[QG], thr[QG];
 #pragma unroll
-        for (int q = 0; q < QG; ++q) S[q] = 0.f;
+        for (int q = 0; q < QG; ++q) {
+            S[q] = 0.f;
+            thr[q] = (m[q] + RESCALE_SLACK) / qr[q].qs;
+        }
         auto fix_v = [&]() {
             if constexpr (C::VFIX) {
 #pragma unroll
@@ -300,8 +303,11 @@ __global__ __launch_bounds__(WAVES * 64, MINB) void decode_tiled(
                 float tmax = sc[q][0];
 #pragma unroll
                 for (int u = 1; u < U; ++u) tmax = fmaxf(tmax, sc[q][u]);
-                tmax *= qr[q].qs;                                      // log2 units
-                if (__builtin_amdgcn_ballot_w64(tmax > m[q] + RESCALE_SLACK)) {
+                // raw scores against thr = (m + RESCALE_SLACK) / qs (wave-uniform,
+                // updated with m); a rounding difference at the threshold only
+                // moves a rescale, which is optional
+                if (__builtin_amdgcn_ballot_w64(tmax > thr[q])) {
+                    tmax *= qr[q].qs;                                  // log2 units
                     const float mn = uniformf(wave_max(fmaxf(m[q], tmax)));
                     const float c  = fast_exp2(m[q] - mn);
                     l[q] *= c;
@@ -309,6 +315,7 @@ __global__ __launch_bounds__(WAVES * 64, MINB) void decode_tiled(
 #pragma unroll
                     for (int e = 0; e < EPL; ++e) o[q][e] *= c;
                     m[q] = mn;
+                    thr[q] = (mn + RESCALE_SLACK) / qr[q].qs;
                 }
             }
 #pragma unroll
@@ -345,17 +352,36 @@ __global__ __launch_bounds__(WAVES * 64, MINB) void decode_tiled(
         // (rem < TW for some wave), so only that tile runs the masked form; the
         // pair loop covers tiles 0 .. 2P-1, all full.
         const int P = (niter - 1) / 2;
-        for (int ip = 0; ip < P; ++ip) {
-            const int it = 2 * ip;
-            if (lockstep) __builtin_amdgcn_s_barrier();     // niter is uniform over the group
-            stage_scales(ska, sva);
-            load_tile(it + 1, kb, vb, skb, svb);
-            compute_tile(std::false_type{}, it, ka, va_);
-            stage_scales(skb, svb);
-            load_tile(it + 2, ka, va_, ska, sva);
-            compute_tile(std::false_type{}, it + 1, kb, vb);
+        // One tile pair: tile it from the A stage, tile it+1 from B, the next
+        // pair's first tile prefetched into A.
+#define VA_PAIR_STEP(it_)                                                     \
+        do {                                                                  \
+            const int it = (it_);                                             \
+            if (lockstep) __builtin_amdgcn_s_barrier();   /* niter is uniform over the group */ \
+            stage_scales(ska, sva);                                           \
+            load_tile(it + 1, kb, vb, skb, svb);                              \
+            compute_tile(std::false_type{}, it, ka, va_);                     \
+            stage_scales(skb, svb);                                           \
+            load_tile(it + 2, ka, va_, ska, sva);                             \
+            compute_tile(std::false_type{}, it + 1, kb, vb);                  \
+        } while (0)
+        // Kinds with a V offset and 2U < 16 rows per lane per pair take
+        // FIXP = 16 / 2U pairs per loop iteration and one offset fix after them:
+        // the window stays <= 16 rows per lane with no branch in the loop body.
+        constexpr int FIXP = C::VFIX && 2 * U < 16 ? 16 / (2 * U) : 1;
+        int ip = 0;
+        if constexpr (FIXP > 1) {
+            for (; ip + FIXP <= P; ip += FIXP) {
+#pragma unroll
+                for (int k = 0; k < FIXP; ++k) VA_PAIR_STEP(2 * (ip + k));
+                fix_v();
+            }
+        }
+        for (; ip < P; ++ip) {
+            VA_PAIR_STEP(2 * ip);
             fix_v();
         }
+#undef VA_PAIR_STEP
         // tail: tile 2P is in the A stage; it is the last one, or one full tile
         // and then the last
         if (niter - 2 * P == 2) {
