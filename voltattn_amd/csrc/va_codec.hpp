@@ -11,8 +11,9 @@
 //   * K (`unpack_k`, `dot`): exact signed values 2^r v as fp16, through the
 //     "magic" construction below, against the fp16 q slice with
 //     v_dot2_f32_f16 (products of two normal fp16 values are exact in fp32;
-//     measured on MI355X, the instruction's sum of two products is then
-//     within 1 fp32 ulp). q is unscaled for f16, q8 and q4 and pre-scaled per
+//     measured on MI355X, the result is within 1 fp32 ulp of |p0| + |p1| on a
+//     zero accumulator and within 16 ulps of |p0| + |p1| + |acc| chained on a
+//     nonzero one). q is unscaled for f16, q8 and q4 and pre-scaled per
 //     element by a power of two for q3. `dot` returns the raw sum; the caller
 //     applies the group scale and qs = log2(e)/sqrt(D) (QReg::qs, uniform
 //     over the wave).
@@ -20,12 +21,13 @@
 //     as an fp16 subnormal c 2^(r-24) (the masked bits alone, exponent field
 //     0: no magic and no subtract), accumulated by v_fma_mix_f32,
 //     o_e += ev * c_e 2^(r_e-24), with an fp16 operand and fp32 accumulation
-//     (P.V stays fp32; the fp16 -> fp32 conversion inside v_fma_mix_f32 keeps
-//     subnormals exactly, measured on MI355X). The offset is removed in bulk:
-//     the caller sums ev over a window of a few rows (S) and `fix_v` adds
-//     S * voff(e) = -OFF 2^(r_e-24) S to each accumulator, so the running sums
-//     never drift more than one window's worth from the signed sums. finish(o)
-//     rescales o_e by 2^(24-r_e) once at the end.
+//     (P.V stays fp32; v_fma_mix_f32 with an fp32 weight and an fp16 code,
+//     subnormal or normal, is one correctly rounded fma: bit-identical to the
+//     host's fmaf in 2^19 random cases on MI355X). The offset is removed in bulk:
+//     the caller sums ev over a window of rows (S; at most 16 per lane) and
+//     `fix_v` adds S * voff(e) = -OFF 2^(r_e-24) S to each accumulator, so the
+//     running sums never drift more than one window's worth from the signed
+//     sums. finish(o) rescales o_e by 2^(24-r_e) once at the end.
 // The magic construction (K): OR-ing a code n (< 2^10 / 2^r) shifted left by r
 // into the mantissa of 1024.0 (0x6400) gives 1024 + 2^r n exactly; one packed
 // fp16 subtract of 1024 + 2^r * offset then leaves 2^r * v. The magic constant
