@@ -96,9 +96,9 @@ typedef struct {
  * and capture sequence while a graph is captured; 16 per device). Calls on
  * different streams may run concurrently; replays of one captured graph must
  * be ordered after each other (as every launch of one executable graph is).
- * When all 16 slots are bound, an eager call may take over the slot of
- * another eager stream that has finished its work; slots of captured graphs
- * are kept until va_graph_destroy or va_capture_release. With H > 1024,
+ * When all 16 slots are bound, a call may take over the slot of an eager
+ * stream that has finished its work; slots of captured graphs are kept until
+ * va_graph_destroy or va_capture_release. With H > 1024,
  * S > 64, H*S > 2048, no slot to be had, or the per-thread default stream
  * (hipStreamPerThread, one handle naming a stream per host thread), the
  * partials go to ws and a separate merge kernel follows. */

@@ -88,6 +88,59 @@ inline void merge(const float* ws, uint16_t* out, int H, int D, int S, void* str
     check(va_merge(ws, out, H, D, S, stream));
 }
 
+// launch() without a workspace (b.ws ignored), for callers that cannot
+// allocate; throws Error with code VA_EBUSY while another stream or graph
+// holds the device's workspace (see va_decode_noalloc).
+inline void launch_noalloc(Fmt f, const DeviceBufs& b, int H, int L, int D, int S, int G = 64,
+                           void* stream = nullptr) {
+    const va_bufs cb = to_c(b);
+    check(va_decode_noalloc(static_cast<va_fmt>(f), &cb, H, L, D, G, S, stream));
+}
+
+// Give back the merge slot and workspace binding of a stream the caller keeps
+// (or of the calling thread's per-thread default stream), or of a graph
+// capture sequence captured outside Graph.
+inline void release_stream(void* stream) { check(va_stream_release(stream)); }
+inline void release_capture(unsigned long long capture_id) { check(va_capture_release(capture_id)); }
+
+// Fused merges that gave up waiting for a partial since the last call (the
+// affected outputs are NaN); synchronises `stream`.
+inline unsigned merge_faults(void* stream = nullptr) {
+    unsigned n = 0;
+    const int rc = va_merge_faults(stream, &n);
+    if (rc != VA_OK && rc != VA_ELOST) check(rc);
+    return n;
+}
+
+// Measurement aids: the read ceiling (GB/s), the size-matched ceiling of one
+// decode step of `bytes` (us per launch, GB/s), one digest-checked probe
+// launch, and the empty-kernel launch floor (us).
+inline double probe_read(size_t bytes, int reps = 5) {
+    double g = 0.0;
+    check(va_probe_read(bytes, reps, &g));
+    return g;
+}
+inline std::pair<double, double> probe_read_sized(size_t bytes, size_t min_set, int launches = 20) {
+    double us = 0.0, g = 0.0;
+    check(va_probe_read_sized(bytes, min_set, launches, &us, &g));
+    return {us, g};
+}
+struct ProbeDigest {
+    uint32_t xor4[4] = {0, 0, 0, 0};
+    uint64_t loads = 0;
+    size_t bytes_read = 0;
+};
+inline ProbeDigest probe_digest(const void* src, size_t bytes, int form, int grid, int unroll) {
+    ProbeDigest d;
+    check(va_probe_digest(src, bytes, form, grid, unroll, d.xor4, &d.loads, &d.bytes_read));
+    return d;
+}
+inline double probe_launch(int launches = 2000) {
+    double us = 0.0;
+    check(va_probe_launch(launches, &us));
+    return us;
+}
+
 inline size_t ws_bytes(int H, int D, int S) { return va_ws_bytes(H, D, S); }
 inline size_t payload_bytes(Fmt f, int H, int L, int D) {
     return va_payload_bytes(static_cast<va_fmt>(f), H, L, D);
