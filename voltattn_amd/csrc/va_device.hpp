@@ -103,6 +103,10 @@ __device__ __forceinline__ float h2f(uint32_t bits16) {
 }
 __device__ __forceinline__ float h2f_lo(uint32_t w) { return h2f(w & 0xFFFFu); }
 __device__ __forceinline__ float h2f_hi(uint32_t w) { return h2f(w >> 16); }
+// Two consecutive fp16 values (lo, hi halves of v) at p, 4-byte aligned.
+__device__ __forceinline__ void store_u32(uint16_t* p, uint32_t v) {
+    *reinterpret_cast<uint32_t*>(p) = v;
+}
 __device__ __forceinline__ uint16_t f2h_rne(float x) {
     return __builtin_bit_cast(uint16_t, (_Float16)x);   // v_cvt_f16_f32, RNE mode
 }
@@ -207,6 +211,29 @@ __device__ __forceinline__ float wave_max(float x) {
 }
 __device__ __forceinline__ float wave_sum(float x) {
     return rows_sum(group_sum<16>(x));
+}
+
+// Sum / max over the 64/PW lanes of a wave that share lane % PW (PW in 1, 2,
+// 4, 8, 16): DPP row rotations by PW, 2PW, .., 8 inside each 16-lane row, then
+// the row swaps. Every lane receives its class's result; the sum's rounding
+// order differs between the lanes of a class, but is fixed for each lane.
+template <int PW>
+__device__ __forceinline__ float column_sum(float x) {
+    static_assert(PW == 1 || PW == 2 || PW == 4 || PW == 8 || PW == 16, "lane class");
+    if constexpr (PW <= 1) x += dpp<dpp_row_ror(1)>(x);
+    if constexpr (PW <= 2) x += dpp<dpp_row_ror(2)>(x);
+    if constexpr (PW <= 4) x += dpp<dpp_row_ror(4)>(x);
+    if constexpr (PW <= 8) x += dpp<dpp_row_ror(8)>(x);
+    return rows_sum(x);
+}
+template <int PW>
+__device__ __forceinline__ float column_max(float x) {
+    static_assert(PW == 1 || PW == 2 || PW == 4 || PW == 8 || PW == 16, "lane class");
+    if constexpr (PW <= 1) x = fmaxf(x, dpp<dpp_row_ror(1)>(x));
+    if constexpr (PW <= 2) x = fmaxf(x, dpp<dpp_row_ror(2)>(x));
+    if constexpr (PW <= 4) x = fmaxf(x, dpp<dpp_row_ror(4)>(x));
+    if constexpr (PW <= 8) x = fmaxf(x, dpp<dpp_row_ror(8)>(x));
+    return rows_max(x);
 }
 
 } // namespace va

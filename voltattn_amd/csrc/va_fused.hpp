@@ -117,176 +117,147 @@ struct Route {
 // o[0..D), and partial (q, s) of merge group mg sits at (mg*QG + q)*S + s.
 // Thread NT-1 (which stores nothing, so its wait covers only its own atomic)
 // takes the group's ticket without waiting for the stores to complete; the
-// work-group that completes the ticket merges. It keeps its own partials in
-// LDS and reads the others with 16-byte coherent loads, each carrying two
-// words; a word whose tag is stale belongs to a group that has already arrived
-// and issued its stores, so it is re-read (bounded) until it lands.
+// work-group that completes the ticket merges. It reads every partial, its
+// own included, with 16-byte coherent loads, each carrying two words; a word
+// whose tag is stale belongs to a group that has already arrived and issued
+// its stores, so it is re-read (bounded) until it lands.
 //
-// The merge spreads the loads over all NT/64 waves (a wave's coherent loads
-// are serviced one instruction at a time; one wave doing all of them measured
-// 0.5-0.9 us slower) and runs the query slots side by side:
-// WQ = NW/QG waves per slot; lane j of each of them reads split j's (m, l),
-// and sub-wave sw folds splits j = sw, sw + WQ, ... in increasing order into
-// lane-pair columns (2i, 2i+1) with split j's weight read by readlane; the WQ
-// sub-wave sums are added in order through LDS. Each wave issues its (m, l)
-// and up to RB o-pair loads together, so the merge waits one round trip. The
-// order is fixed, so the result does not depend on arrival order. A merged l of zero
-// (no positions) gives a zero output; a non-finite one (an invalid input that
-// the kernel flagged with l = NaN) gives NaN. Needs S <= 64.
+// A lone merging wave issues one instruction every few cycles, so the merge is
+// written for few instructions per wave. Wave w of the NW = NT/64 waves owns
+// the PW = D/2/NW o-pair columns [w*PW, (w+1)*PW) of the output: lane (jj, c)
+// of its i-th load pair reads split j = i*SPI + jj (SPI = 64/PW splits per
+// instruction): the (m, l) words and the o pair of column w*PW + c. Each lane
+// weights its own splits (exp2(m_j - M), M the maximum over all splits); the
+// lanes of a column are summed by a fixed butterfly (DPP row rotations, then
+// the row swaps of rows_sum), which also sums l, and the wave stores its own
+// columns: no LDS and no barrier after the ticket. Up to RB*SPI splits are
+// held at once; more are folded in batches with the running maximum
+// rescaled. The order is fixed, so the result does not depend on arrival
+// order. A merged l of zero (no positions) gives a zero output; a non-finite
+// one (an invalid input that the kernel flagged with l = NaN) gives NaN.
+// Needs S <= 64.
 template <int D, int NT, int QG>
 __device__ void finish_tagged(const DecodeArgs& a, const Route& rt, const float (&M)[QG],
                               const float (&ls)[QG], const float (&acc)[QG], unsigned epoch) {
+    static_assert(QG == 1, "the tagged protocol merges one query slot per work-group");
     constexpr int NW = NT / 64;
+    constexpr int PW = D / 2 / NW;              // o pairs (columns) per wave
+    constexpr int SPI = 64 / PW;                // splits per load instruction
+    constexpr int RB = 4;                       // load pairs per batch
     constexpr uint32_t PB = PART_STRIDE * 8;    // bytes per partial (16-byte multiple)
     static_assert(PB % 16 == 0 && D + 2 <= PART_STRIDE, "partial layout");
+    static_assert(PW >= 1 && PW <= 16 && (PW & (PW - 1)) == 0 && D / 2 == PW * NW, "columns per wave");
     const int t = (int)threadIdx.x;
     const int S = a.S, s = rt.s;
-    // The merge splits the NW waves over the query slots: WQ = NW / QG waves per
-    // slot (all waves on one slot when QG = 1); wave w merges slot w / WQ and
-    // folds its splits j = sw, sw + WQ, ... (sw = w % WQ) in increasing order.
-    constexpr int WQ = NW / QG;
-    static_assert(NW >= QG && NW % QG == 0, "whole waves per query slot");
-    // o-pair loads per wave per batch: a batch covers a slot's splits in the
-    // grouped forms; with one slot (the reference shape) a small batch keeps
-    // the register count, and so the occupancy, of the split pass.
-    constexpr int RB = QG > 1 ? 16 : 4;
-    __shared__ int   s_last, s_bad;
-    __shared__ float s_own[QG][D + 2];          // o[0..D), m, l of this group's partials
-    __shared__ float s_fold[QG][WQ][D];
-    __shared__ float s_lsum[QG];
+    __shared__ int s_last;
     unsigned* ticket = g_tickets + ((size_t)a.ticket_slot * TICKET_MAXH + rt.mg) * TICKET_STRIDE;
     if (t == NT - 1)
         s_last = __hip_atomic_fetch_add(ticket, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
                  (unsigned)(S - 1);
     const uint32_t tag = part_tag(epoch, S);
     const uint32_t want = VA_TEST_LOSE_MERGES ? tag ^ 0x80000000u : tag;   // the merger's expected tag
-    uint64_t* base = g_parts + ((size_t)a.ticket_slot * PART_CAP + (size_t)rt.mg * QG * S) * PART_STRIDE;
-    if (t < D) {
-#pragma unroll
-        for (int q = 0; q < QG; ++q) {
-            if (q >= rt.nq) break;
-            uint64_t* mine = base + ((size_t)q * S + s) * PART_STRIDE;
-            store_dev(mine + 2 + t, tagged(acc[q], tag));
-            s_own[q][t] = acc[q];
-            if (t == 0) {
-                store_dev(mine, tagged(M[q], tag));
-                store_dev(mine + 1, tagged(ls[q], tag));
-                s_own[q][D] = M[q];
-                s_own[q][D + 1] = ls[q];
-            }
+    uint64_t* base = g_parts + ((size_t)a.ticket_slot * PART_CAP + (size_t)rt.mg * S) * PART_STRIDE;
+    if (t < D && rt.nq > 0) {
+        uint64_t* mine = base + (size_t)s * PART_STRIDE;
+        store_dev(mine + 2 + t, tagged(acc[0], tag));
+        if (t == 0) {
+            store_dev(mine, tagged(M[0], tag));
+            store_dev(mine + 1, tagged(ls[0], tag));
         }
-        if (t == 0) s_bad = 0;
     }
     __syncthreads();
     if (!s_last) return;
 
     const int w    = uniform(t >> 6);
     const int lane = t & 63;
-    const int qw   = w / WQ, sw = w - (w / WQ) * WQ;
-    const int dp   = min(lane, D / 2 - 1);     // o pair of this lane: dims 2dp, 2dp + 1
-    const int jl   = min(lane, S - 1);
-    const bool in_s = lane < S, own = lane == s;
-    bool good = true;
-    if (qw < rt.nq) {                            // wave-uniform
-        const __amdgpu_buffer_rsrc_t rp = make_rsrc(base + (size_t)qw * S * PART_STRIDE, (uint32_t)S * PB);
-        const int nsw = (S - sw + WQ - 1) / WQ;  // splits folded by this wave
-        uint32_t op[RB][4];
-        auto load_batch = [&](int b0) {
+    const int c    = w * PW + (lane % PW);      // this lane's o pair: dims 2c, 2c + 1
+    const int jj   = lane / PW;                 // split within a load instruction
+    const int ninst = (S + SPI - 1) / SPI;      // load pairs per wave (wave-uniform)
+    const __amdgpu_buffer_rsrc_t rp = make_rsrc(base, (uint32_t)S * PB);
+    float mx = 0.f, o0 = 0.f, o1 = 0.f, lw = 0.f;
+    uint32_t stale = 0;
+    for (int b0 = 0; b0 < ninst; b0 += RB) {     // one batch up to S = RB*SPI
+        // The words are taken out of each 16-byte vector right after its load
+        // (carrying the vectors through the re-read loop was mis-compiled).
+        uint32_t mv[RB], mt[RB], lv[RB], lt[RB], a0[RB], t0[RB], a1[RB], t1[RB];
+        auto load = [&]() {
 #pragma unroll
             for (int i = 0; i < RB; ++i) {
-                const int j = sw + WQ * (b0 + i);  // wave-uniform: no load past the last split
-                if (b0 + i < nsw) {
-                    const u32x4 x = ld128_dev(rp, (uint32_t)j * PB + 16u + (uint32_t)dp * 16u);
-                    op[i][0] = x.x; op[i][1] = x.y; op[i][2] = x.z; op[i][3] = x.w;
+                if (b0 + i < ninst) {           // wave-uniform
+                    // lanes past S re-read split S-1 (weight 0)
+                    const uint32_t off = (uint32_t)min((b0 + i) * SPI + jj, S - 1) * PB;
+                    const u32x4 x = ld128_dev(rp, off);
+                    mv[i] = x.x; mt[i] = x.y; lv[i] = x.z; lt[i] = x.w;
+                    const u32x4 y = ld128_dev(rp, off + 16u + (uint32_t)c * 16u);
+                    a0[i] = y.x; t0[i] = y.y; a1[i] = y.z; t1[i] = y.w;
                 }
             }
         };
-        // (m, l) of split `lane` (words 0, 1 of its partial) and the first batch
-        // of o pairs are issued together (the compiler barrier keeps the loads
-        // from being sunk to their uses). The words are taken out of each 16-byte
-        // vector right after its load (carrying the vector through the re-read
-        // loop was mis-compiled).
-        const u32x4 ml = ld128_dev(rp, (uint32_t)jl * PB);
-        uint32_t mv = ml.x, mt = ml.y, lv = ml.z, lt = ml.w;
-        load_batch(0);
-        asm volatile("" ::: "memory");
-        // Selection is branch-free and the rare re-read loop is wave-uniform (all
-        // lanes run it, stale lanes take the new value).
-        for (int k = 0; k < POLL_MAX; ++k) {     // rare: stores still in flight
-            const bool need = in_s && !own && !(mt == want && lt == want);
-            if (__builtin_amdgcn_ballot_w64(need) == 0) break;
-            __builtin_amdgcn_s_sleep(2);
-            const u32x4 re = ld128_dev(rp, (uint32_t)jl * PB);
-            const uint32_t rmv = re.x, rmt = re.y, rlv = re.z, rlt = re.w;
-            mv = need ? rmv : mv;
-            mt = need ? rmt : mt;
-            lv = need ? rlv : lv;
-            lt = need ? rlt : lt;
-        }
-        good = good && (!in_s || own || (mt == want && lt == want));
-        const float own_m = s_own[qw][D], own_l = s_own[qw][D + 1];
-        const float mj = !in_s ? -__builtin_inff() : own ? own_m : __builtin_bit_cast(float, mv);
-        const float lj = !in_s ? 0.f : own ? own_l : __builtin_bit_cast(float, lv);
-        const float mx = wave_max(mj);
-        const float wj = fast_exp2(mj - mx);    // weight of split `lane` (0 past S)
-        const float lsum = wave_sum(wj * lj);
-        float o0 = 0.f, o1 = 0.f;
-        for (int b0 = 0; b0 < nsw; b0 += RB) {
-            if (b0 != 0) load_batch(b0);         // splits beyond the first batch (S > RB * WQ)
+        auto stale_words = [&]() {
+            uint32_t x = 0;
 #pragma unroll
-            for (int i = 0; i < RB; ++i) {
-                if (b0 + i >= nsw) break;        // wave-uniform
-                const int j = sw + WQ * (b0 + i);
-                float v0, v1;
-                if (j == s) {                    // wave-uniform
-                    v0 = s_own[qw][2 * dp];
-                    v1 = s_own[qw][2 * dp + 1];
-                } else {
-                    uint32_t a0 = op[i][0], t0 = op[i][1], a1 = op[i][2], t1 = op[i][3];
-                    for (int k = 0; k < POLL_MAX; ++k) {
-                        const bool need = !(t0 == want && t1 == want);
-                        if (__builtin_amdgcn_ballot_w64(need) == 0) break;
-                        __builtin_amdgcn_s_sleep(2);
-                        const u32x4 re = ld128_dev(rp, (uint32_t)j * PB + 16u + (uint32_t)dp * 16u);
-                        const uint32_t ra0 = re.x, rt0 = re.y, ra1 = re.z, rt1 = re.w;
-                        a0 = need ? ra0 : a0;
-                        t0 = need ? rt0 : t0;
-                        a1 = need ? ra1 : a1;
-                        t1 = need ? rt1 : t1;
-                    }
-                    good = good && t0 == want && t1 == want;
-                    v0 = __builtin_bit_cast(float, a0);
-                    v1 = __builtin_bit_cast(float, a1);
-                }
-                const float f = __builtin_bit_cast(float,
-                    __builtin_amdgcn_readlane(__builtin_bit_cast(int, wj), j));
-                o0 = __builtin_fmaf(f, v0, o0);
-                o1 = __builtin_fmaf(f, v1, o1);
+            for (int i = 0; i < RB; ++i)
+                if (b0 + i < ninst) x |= (mt[i] ^ want) | (lt[i] ^ want) | (t0[i] ^ want) | (t1[i] ^ want);
+            return x;
+        };
+        load();
+        uint32_t st = stale_words();
+        // Rare: a partial's stores still in flight. The loop is wave-uniform
+        // and re-reads the whole batch (current words stay current).
+        for (int k = 0; k < POLL_MAX; ++k) {
+            if (__builtin_amdgcn_ballot_w64(st != 0) == 0) break;
+            __builtin_amdgcn_s_sleep(2);
+            load();
+            st = stale_words();
+        }
+        stale |= st;
+        float mi[RB];
+        float bm = -__builtin_inff();
+#pragma unroll
+        for (int i = 0; i < RB; ++i) {
+            if (b0 + i < ninst) {
+                mi[i] = (b0 + i) * SPI + jj < S ? __builtin_bit_cast(float, mv[i]) : -__builtin_inff();
+                bm = fmaxf(bm, mi[i]);
             }
         }
-        if (lane < D / 2) {
-            s_fold[qw][sw][2 * lane]     = o0;
-            s_fold[qw][sw][2 * lane + 1] = o1;
+        bm = column_max<PW>(bm);                 // over every split of the batch
+        if (b0 == 0) {
+            mx = bm;
+        } else {
+            const float mn = fmaxf(mx, bm);
+            const float r = fast_exp2(mx - mn);
+            o0 *= r;
+            o1 *= r;
+            lw *= r;
+            mx = mn;
         }
-        if (sw == 0 && lane == 0) s_lsum[qw] = lsum;
-    }
-    // A lost partial (never observed within the poll bound) shows as NaN, and
-    // is counted for the host (va_merge_faults).
-    if (__builtin_amdgcn_ballot_w64(!good) != 0 && lane == 0) s_bad = 1;
-    __syncthreads();
-    if (t == 0 && s_bad) count_lost_merge();
-    if (t < D) {
 #pragma unroll
-        for (int q = 0; q < QG; ++q) {
-            if (q >= rt.nq) break;
-            float o = 0.f;
-#pragma unroll
-            for (int v = 0; v < WQ; ++v) o += s_fold[q][v][t];
-            const float r = s_lsum[q] == 0.f ? 0.f : o / s_lsum[q];
-            a.out[(size_t)(rt.oh0 + q) * D + t] = s_bad ? (uint16_t)0x7E00u : f2h_rne(r);
+        for (int i = 0; i < RB; ++i) {
+            if (b0 + i < ninst) {
+                const float f = fast_exp2(mi[i] - mx);       // 0 past S
+                o0 = __builtin_fmaf(f, __builtin_bit_cast(float, a0[i]), o0);
+                o1 = __builtin_fmaf(f, __builtin_bit_cast(float, a1[i]), o1);
+                lw = __builtin_fmaf(f, __builtin_bit_cast(float, lv[i]), lw);
+            }
         }
     }
-    if (t == 0) {                            // every arrival is in: reset for the slot's next call
+    o0 = column_sum<PW>(o0);
+    o1 = column_sum<PW>(o1);
+    lw = column_sum<PW>(lw);
+    // A lost partial (never observed within the poll bound) shows as NaN in the
+    // columns of every wave that saw it. Every wave reads every split's (m, l),
+    // so a partial that never landed is seen by wave 0, which counts the merge
+    // once for the host (va_merge_faults).
+    const bool bad = __builtin_amdgcn_ballot_w64(stale != 0) != 0;
+    if (lane < PW && rt.nq > 0) {
+        const float r = lw == 0.f ? 0.f : 1.f / lw;
+        const uint32_t h = bad ? 0x7E007E00u : ((uint32_t)f2h_rne(o0 * r) | ((uint32_t)f2h_rne(o1 * r) << 16));
+        store_u32(a.out + (size_t)rt.oh0 * D + 2 * c, h);
+    }
+    // Every arrival is in: reset the slot for its next call (which runs after
+    // this kernel, so no other wave needs to have finished).
+    if (t == 0) {
+        if (bad) count_lost_merge();
         store_dev(ticket, 0u);
         store_dev(ticket + 1, epoch + 1u);
     }
