@@ -27,7 +27,11 @@
 //     the caller sums ev over a window of rows (S; at most 16 per lane) and
 //     `fix_v` adds S * voff(e) = -OFF 2^(r_e-24) S to each accumulator, so the
 //     running sums never drift more than one window's worth from the signed
-//     sums. finish(o) rescales o_e by 2^(24-r_e) once at the end.
+//     sums. fin(e) = 2^(24-r_e) rescales o_e once at the end; the caller folds
+//     it into the last fix, o_e = fma(o_e, fin(e), S * voff(e) * fin(e)), which
+//     is fin(e) * (o_e + S * voff(e)) rounded once, as fix then rescale
+//     (fin(e) and voff(e) * fin(e) = -OFF are powers of two or small integers,
+//     so S * voff(e) * fin(e) is exact).
 // The magic construction (K): OR-ing a code n (< 2^10 / 2^r) shifted left by r
 // into the mantissa of 1024.0 (0x6400) gives 1024 + 2^r n exactly; one packed
 // fp16 subtract of 1024 + 2^r * offset then leaves 2^r * v. The magic constant
@@ -40,7 +44,7 @@
 // Interface: QReg (one query head's slice in codec form, with qs),
 // load_q<LP>(QReg&, q slice, qs) (LP: lanes per row), magic(), unpack_k(w, magic, p[NP]), dot(p, QReg) -> raw q.k,
 // unpack_v(w, p[NP]), axpy_v(p, ev, o), VFIX / voff(e) (bulk offset removal),
-// finish(o) (per-element rescale once at the end).
+// fin(e) (per-element rescale once at the end).
 #pragma once
 #include "va_device.hpp"
 
@@ -147,7 +151,7 @@ template <> struct Codec<KF16> {
     __device__ static constexpr float voff(int) { return 0.f; }
     __device__ static void unpack_v(const u32x4& w, h2 (&p)[NP]) { unpack_k(w, 0u, p); }
     __device__ static void axpy_v(const h2 (&p)[NP], float ev, float* o) { axpy_pairs<NP>(p, ev, o); }
-    __device__ static void finish(float*) {}
+    __device__ static constexpr float fin(int) { return 1.f; }
 };
 
 // q8: 16 int8 per lane, element 4i+b in byte b of dword i. xor 0x80 makes the
@@ -187,10 +191,7 @@ template <> struct Codec<KQ8> {
         }
     }
     __device__ static void axpy_v(const h2 (&p)[NP], float ev, float* o) { axpy_pairs<NP>(p, ev, o); }
-    __device__ static void finish(float* o) {
-#pragma unroll
-        for (int e = 0; e < EPL; ++e) o[e] *= 16777216.f;
-    }
+    __device__ static constexpr float fin(int) { return 16777216.f; }
 };
 
 // q4: 32 nibbles per lane; element 8i+j sits in nibble j of dword i. Masking
@@ -264,10 +265,7 @@ template <> struct Codec<KQ4> {
             }
         }
     }
-    __device__ static void finish(float* o) {
-#pragma unroll
-        for (int e = 0; e < EPL; ++e) o[e] *= (e & 1) ? 1048576.f : 16777216.f;
-    }
+    __device__ static constexpr float fin(int e) { return (e & 1) ? 1048576.f : 16777216.f; }
 };
 
 // q3: 32 3-bit fields per lane, element e at bits [3e, 3e+3) of the lane's
@@ -282,7 +280,7 @@ template <> struct Codec<KQ4> {
 // power of two k (max |q| * 2^k in [2^14, 2^15) over the whole head, so qs is
 // the same in every lane) keeps every scaled q that matters normal; 2^-k is
 // folded into qs. For V the masked window alone is the subnormal pair
-// (c 2^(r-24), c' 2^(r'-24)), OFF = 4, and finish() scales o_e by 2^(24-r).
+// (c 2^(r-24), c' 2^(r'-24)), OFF = 4, and fin(e) = 2^(24-r).
 struct Q3Pair { int a, b, s, r, rp; };
 __device__ constexpr Q3Pair kQ3Pairs[16] = {
     {0, 6, 0, 0, 2},    {1, 7, 0, 3, 5},    {2, 8, 6, 0, 2},    {3, 9, 6, 3, 5},
@@ -377,10 +375,7 @@ template <> struct Codec<KQ3> {
             o[kQ3Pairs[i].b] = __builtin_fmaf(ev, (float)p[i].y, o[kQ3Pairs[i].b]);
         }
     }
-    __device__ static void finish(float* o) {
-#pragma unroll
-        for (int e = 0; e < 32; ++e) o[e] *= 16777216.f / (float)(1 << q3_shift(e));
-    }
+    __device__ static constexpr float fin(int e) { return 16777216.f / (float)(1 << q3_shift(e)); }
 };
 
 } // namespace va

@@ -63,6 +63,24 @@ __device__ constexpr float qscale_of() {
 // without waiting for a kernarg fetch; dst (`out` for the fused merge, slot
 // >= 0; `ws` for the two-pass form) and `rest` (grouped-query and paged
 // fields) are read from the kernarg segment when needed.
+// The last offset fix and the codec's rescale of one accumulator, one fma with
+// compile-time constants: fma(o, fin(e), S * voff(e) * fin(e)) is exactly
+// fix_v() followed by o *= fin(e) (va_codec.hpp).
+template <class C, int E>
+__device__ __forceinline__ void fix_finish_one(float& o, float s) {
+    constexpr float f = C::fin(E);
+    if constexpr (C::VFIX) {
+        constexpr float k = C::voff(E) * C::fin(E);
+        o = __builtin_fmaf(o, f, s * k);
+    } else {
+        o *= f;
+    }
+}
+template <class C, int... E>
+__device__ __forceinline__ void fix_finish(float* o, float s, std::integer_sequence<int, E...>) {
+    (fix_finish_one<C, E>(o[E], s), ...);
+}
+
 template <int KIND, int D, int G, int U, int WAVES, int QG, bool PAGED, int MINB = 1>
 __global__ __launch_bounds__(WAVES * 64, MINB) void decode_tiled(
     const uint8_t* k, const uint8_t* v, const uint16_t* sk, const uint16_t* sv,
@@ -394,9 +412,8 @@ __global__ __launch_bounds__(WAVES * 64, MINB) void decode_tiled(
             stage_scales(ska, sva);
             compute_tile(std::true_type{}, 2 * P, ka, va_);
         }
-        fix_v();
 #pragma unroll
-        for (int q = 0; q < QG; ++q) C::finish(o[q]);
+        for (int q = 0; q < QG; ++q) fix_finish<C>(o[q], S[q], std::make_integer_sequence<int, EPL>{});
     }
 
     // ---- work-group merge: slots of a DPP row first, then rows/waves via LDS.
@@ -409,6 +426,12 @@ __global__ __launch_bounds__(WAVES * 64, MINB) void decode_tiled(
             if (off == 4) { l[q] += dpp<dpp_row_ror(4)>(l[q]); for (int e = 0; e < EPL; ++e) o[q][e] += dpp<dpp_row_ror(4)>(o[q][e]); }
             if (off == 8) { l[q] += dpp<dpp_row_ror(8)>(l[q]); for (int e = 0; e < EPL; ++e) o[q][e] += dpp<dpp_row_ror(8)>(o[q][e]); }
         }
+        // The sums are used only by the lanes that write them out; computed
+        // here in every lane, each add stays one DPP instruction (sunk into
+        // the write-out branch it would be a DPP move plus an add).
+        asm volatile("" : "+v"(l[q]));
+#pragma unroll
+        for (int e = 0; e < EPL; ++e) asm volatile("" : "+v"(o[q][e]));
     }
     const int row = lane >> 4;
     if ((lane & 15) < LP) {                       // one slot per 16-lane row holds the row sum
