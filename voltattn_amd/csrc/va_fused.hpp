@@ -250,7 +250,8 @@ __device__ void finish_tagged(const DecodeArgs& a, const Route& rt, const float 
     // once for the host (va_merge_faults).
     const bool bad = __builtin_amdgcn_ballot_w64(stale != 0) != 0;
     if (lane < PW && rt.nq > 0) {
-        const float r = lw == 0.f ? 0.f : 1.f / lw;
+        // v_rcp_f32 (1 ulp): the fp16 result is rounded from o * r
+        const float r = lw == 0.f ? 0.f : __builtin_amdgcn_rcpf(lw);
         const uint32_t h = bad ? 0x7E007E00u : ((uint32_t)f2h_rne(o0 * r) | ((uint32_t)f2h_rne(o1 * r) << 16));
         store_u32(a.out + (size_t)rt.oh0 * D + 2 * c, h);
     }

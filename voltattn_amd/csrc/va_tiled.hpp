@@ -108,7 +108,7 @@ __global__ __launch_bounds__(WAVES * 64, MINB) void decode_tiled(
 
     __shared__ uint32_t s_scale[WAVES][SCN];
     __shared__ float    s_red[QG][WAVES * 4][D + 1];
-    __shared__ float    s_l[QG][WAVES * 4];
+    __shared__ float    s_l[QG][WAVES];
     __shared__ float    s_m[QG][WAVES];
     __shared__ int      s_page[PAGED ? MAX_SPLIT_PAGES : 1];
 
@@ -439,12 +439,19 @@ __global__ __launch_bounds__(WAVES * 64, MINB) void decode_tiled(
         for (int q = 0; q < QG; ++q) {
 #pragma unroll
             for (int e = 0; e < EPL; ++e) s_red[q][wave * 4 + row][sl * EPL + e] = o[q][e];
-            if (sl == 0) s_l[q][wave * 4 + row] = l[q];
         }
     }
+    // l: every lane holds its row's sum; the rows are summed in the wave (row
+    // swaps), so the fold below takes one l per wave.
+    float lw[QG];
+#pragma unroll
+    for (int q = 0; q < QG; ++q) lw[q] = rows_sum(l[q]);
     if (lane == 0) {
 #pragma unroll
-        for (int q = 0; q < QG; ++q) s_m[q][wave] = m[q];
+        for (int q = 0; q < QG; ++q) {
+            s_m[q][wave] = m[q];
+            s_l[q][wave] = lw[q];
+        }
     }
     // A bad tile in any wave marks every partial of the group (l = NaN).
     bool any_bad = false;
@@ -470,7 +477,7 @@ __global__ __launch_bounds__(WAVES * 64, MINB) void decode_tiled(
 #pragma unroll
                 for (int r = 0; r < WAVES * 4; ++r) acc[q] = __builtin_fmaf(f[r / 4], s_red[q][r][t], acc[q]);
 #pragma unroll
-                for (int r = 0; r < WAVES * 4; ++r) ls[q] = __builtin_fmaf(f[r / 4], s_l[q][r], ls[q]);
+                for (int w = 0; w < WAVES; ++w) ls[q] = __builtin_fmaf(f[w], s_l[q][w], ls[q]);
                 if (any_bad) ls[q] = __builtin_nanf("");
             }
         }
@@ -492,7 +499,7 @@ __global__ __launch_bounds__(WAVES * 64, MINB) void decode_tiled(
             s_acc[q][d] = sacc;
             if (d == 0) {
 #pragma unroll
-                for (int r = 0; r < WAVES * 4; ++r) sl = __builtin_fmaf(f[r / 4], s_l[q][r], sl);
+                for (int w = 0; w < WAVES; ++w) sl = __builtin_fmaf(f[w], s_l[q][w], sl);
                 s_mf[q] = m;
                 s_lf[q] = any_bad ? __builtin_nanf("") : sl;
             }
