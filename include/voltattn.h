@@ -223,7 +223,8 @@ int va_probe_digest(const void* src, size_t bytes, int form, int grid, int unrol
  * va_probe_read over exactly `bytes` per launch with one or two 4-wave groups
  * per CU (the decode grid), `launches` launches back to back on one stream
  * between two events, rotating over copies that together span >= min_set
- * bytes (so the Infinity Cache cannot serve them), after a warm-up; the best
+ * bytes (so the Infinity Cache cannot serve them), each shape after at least
+ * 50 ms of untimed launches (the clocks leave their idle level); the best
  * mean over the chunked shapes. Returns microseconds per launch and bytes /
  * that time in GB/s: what any kernel that reads that many bytes per launch
  * pays, launch gap, ramp and tail included. No counterpart in the reference

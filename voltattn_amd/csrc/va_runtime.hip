@@ -11,6 +11,7 @@
 
 #include <algorithm>
 #include <atomic>
+#include <chrono>
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
@@ -905,7 +906,9 @@ int va_probe_read_sized(size_t bytes, size_t min_set, int launches, double* us_p
         }
         // The chunked form's four shapes (1 or 2 groups per CU, 4 or 8 loads per
         // lane in flight), each `launches` back to back over rotating copies;
-        // the best mean is the ceiling.
+        // the best mean is the ceiling. Each shape first runs untimed for at
+        // least 50 ms of wall time: an idle MI355X sits near its lowest clocks,
+        // and a cold 142.6 MB read measured ~2 us (9 %) slower per launch.
         for (int gpc = 1; gpc <= 2 && e == hipSuccess; ++gpc) {
             for (int un : {4, 8}) {
                 size_t c = 0;
@@ -913,6 +916,12 @@ int va_probe_read_sized(size_t bytes, size_t min_set, int launches, double* us_p
                     const void* p = static_cast<const uint8_t*>(src) + (c++ % copies) * stride;
                     return va::launch_probe_chunks(p, bytes, dig, cus * gpc, un, st);
                 };
+                const auto warm_end = std::chrono::steady_clock::now() + std::chrono::milliseconds(50);
+                for (int batch = 0; batch < 4096 && e == hipSuccess; ++batch) {
+                    for (int i = 0; i < 16 && e == hipSuccess; ++i) e = launch();
+                    if (e == hipSuccess) e = hipStreamSynchronize(st);
+                    if (std::chrono::steady_clock::now() >= warm_end) break;
+                }
                 for (int i = 0; i < 5 && e == hipSuccess; ++i) e = launch();
                 if (e == hipSuccess) e = hipStreamSynchronize(st);
                 if (e == hipSuccess) e = hipEventRecord(e0, st);
