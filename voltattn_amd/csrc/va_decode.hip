@@ -112,13 +112,14 @@ __global__ __launch_bounds__(256) void decode_w1(DecodeArgs a) {
 
 // ---------------------------------------------------------------- dispatch --
 // Tiled configuration per kind: waves per group and tile depth (UnrollSet a or
-// b), measured at H=32 D=128 over L = 4K..64K on MI355X. Every default keeps
-// the same bytes in flight per CU (8 waves x depth a); fewer, deeper groups
-// mean fewer partials to merge and a shorter dispatch. The configuration is
-// fixed at compile time (VA_<KIND>_WAVES = 4|8, VA_<KIND>_DEEP = 0|1 build
-// variants); only the configured kernel of each kind is built.
+// b), measured at H=32 D=128 over L = 4K..64K on MI355X, one group per CU.
+// The configuration is fixed at compile time (VA_<KIND>_WAVES = 4|8,
+// VA_<KIND>_DEEP = 0|1 build variants); only the configured kernel of each
+// kind is built. f16 in 4-wave groups (the waves interleaved by load, as every
+// contiguous 4-wave group) against 8-wave groups: L 4096 13.65 -> 13.26 us,
+// 16384 41.71 -> 40.97, 65536 155.3 -> 153.0.
 #ifndef VA_F16_WAVES
-#define VA_F16_WAVES 8               // 8 waves x 4 rows
+#define VA_F16_WAVES 4               // 4 waves x 4 rows
 #endif
 #ifndef VA_F16_DEEP
 #define VA_F16_DEEP 0
@@ -158,11 +159,6 @@ static int tiled_positions() {
     return Tile<KIND, D>::PPW * TiledShape<KIND>::U * TiledShape<KIND>::waves;
 }
 
-template <int KIND>
-static int tiled_groups() {
-    return std::max(1, 8 * UnrollSet<KIND>::a / (TiledShape<KIND>::waves * TiledShape<KIND>::U));
-}
-
 int tile_positions(int kind, bool tiled, int D) {
     if (!tiled) return WAVES;
     switch (kind) {
@@ -173,14 +169,12 @@ int tile_positions(int kind, bool tiled, int D) {
     }
 }
 
+// Tiled kinds: one work-group per CU. A second group per CU (twice the
+// splits) measured slower on MI355X with every configured shape (f16+ at
+// L 16384: 42.91 against 40.97 us; q8+ and q4+ at S = 16, 32, 64 too).
 int groups_per_cu(int kind, bool tiled) {
-    if (!tiled) return 8;                 // naive: one position per wave, 32 waves per CU
-    switch (kind) {
-        case KF16: return tiled_groups<KF16>();
-        case KQ8:  return tiled_groups<KQ8>();
-        case KQ4:  return tiled_groups<KQ4>();
-        default:   return tiled_groups<KQ3>();
-    }
+    (void)kind;
+    return tiled ? 1 : 8;                 // naive: one position per wave, 32 waves per CU
 }
 
 template <int KIND, int D, int G>

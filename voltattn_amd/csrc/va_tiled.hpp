@@ -103,6 +103,18 @@ __global__ __launch_bounds__(WAVES * 64, MINB) void decode_tiled(
     constexpr int SCN = QUANT ? TW * NG : 1;     // (k, v) scale pairs per wave tile
     constexpr int SCE = !QUANT ? 1 : NG >= 2 ? SCN / 2 : SCN;  // scale dwords/halves per tensor
     constexpr int SCR = (SCE + 63) / 64;         // scale loads per lane per tensor
+    // Rows of a work-group tile. Contiguous 4-wave groups interleave the waves
+    // by load instruction: load u of wave w reads rows u*PPW*WAVES + w*PPW ..
+    // + PPW, so the group's u-th loads cover WAVES*PPW consecutive rows
+    // (measured on MI355X, H=32 D=128: q8+ L 16384 24.85 -> 24.49 us, 65536
+    // 85.8 -> 85.0, q4+ 16384 16.30 -> 16.04). 8-wave groups keep each wave's
+    // TW rows together (interleaved, f16+ at 16384 took 47.5 against 41.8 us),
+    // and so does the paged form (a wave tile lies in one page).
+    // RS = rows between a wave's loads, WS = rows between waves.
+    constexpr bool IL = !PAGED && WAVES == 4;
+    constexpr int RS = IL ? PPW * WAVES : PPW;
+    constexpr int WS = IL ? PPW : TW;
+    constexpr int SPG = NG >= 2 ? PPW * NG / 2 : PPW;  // scale entries of one load's rows
     static_assert(!QUANT || G % EPL == 0, "a lane's elements share one scale group");
     static_assert(SCE % 64 == 0 || SCR == 1, "scale entries fill whole wave loads");
 
@@ -188,7 +200,7 @@ __global__ __launch_bounds__(WAVES * 64, MINB) void decode_tiled(
         // Issue order is pinned (scales, then K, then V) so the prologue and the
         // loop leave the same pending-load sequence and the waits stay partial.
         auto load_tile = [&](int it, LoadT* kk, LoadT* vv, uint32_t* sk, uint32_t* sv) {
-            const int t0 = it * TB + wave * TW;                 // tile's first row in the split
+            const int t0 = it * TB + wave * WS;                 // wave's first row in the split
             __amdgpu_buffer_rsrc_t tk = rk, tv = rv, tsk = rsk, tsv = rsv;
             uint32_t soff = (uint32_t)t0;
             if constexpr (PAGED) {
@@ -216,21 +228,23 @@ __global__ __launch_bounds__(WAVES * 64, MINB) void decode_tiled(
 #pragma unroll
                 for (int r = 0; r < SCR; ++r) {
                     const uint32_t sidx = (uint32_t)min(lane + 64 * r, SCE - 1);
+                    // entry sidx belongs to the rows of load sidx / SPG
+                    const uint32_t gap = (sidx / SPG) * (uint32_t)(RS - PPW) * NG * 2;   // bytes
                     if constexpr (NG >= 2) {
-                        sk[r] = ld32(tsk, sidx * 4, tpos * NG * 2);
-                        sv[r] = ld32(tsv, sidx * 4, tpos * NG * 2);
+                        sk[r] = ld32(tsk, sidx * 4 + gap, tpos * NG * 2);
+                        sv[r] = ld32(tsv, sidx * 4 + gap, tpos * NG * 2);
                     } else {
-                        sk[r] = ld16(tsk, sidx * 2, tpos * 2);
-                        sv[r] = ld16(tsv, sidx * 2, tpos * 2);
+                        sk[r] = ld16(tsk, sidx * 2 + gap, tpos * 2);
+                        sv[r] = ld16(tsv, sidx * 2 + gap, tpos * 2);
                     }
                 }
             }
 #pragma unroll
             for (int u = 0; u < U; ++u)
-                kk[u] = lane_load<KIND>(tk, lane_off + (uint32_t)(u * PPW * ROWB), tpos * ROWB);
+                kk[u] = lane_load<KIND>(tk, lane_off + (uint32_t)(u * RS * ROWB), tpos * ROWB);
 #pragma unroll
             for (int u = 0; u < U; ++u)
-                vv[u] = lane_load<KIND>(tv, lane_off + (uint32_t)(u * PPW * ROWB), tpos * ROWB);
+                vv[u] = lane_load<KIND>(tv, lane_off + (uint32_t)(u * RS * ROWB), tpos * ROWB);
             __builtin_amdgcn_sched_barrier(0);
         };
 
@@ -309,12 +323,12 @@ __global__ __launch_bounds__(WAVES * 64, MINB) void decode_tiled(
             }
             // Rows past the split end score -inf (the masked form of the loop).
             if constexpr (MASK) {
-                const int rem = uniform(n - it * TB - wave * TW);   // valid rows of this wave tile
+                const int rem = uniform(n - it * TB - wave * WS);   // rows of the split from the wave's first
 #pragma unroll
                 for (int u = 0; u < U; ++u)
 #pragma unroll
                     for (int q = 0; q < QG; ++q)
-                        sc[q][u] = u * PPW + pw < rem ? sc[q][u] : -__builtin_inff();
+                        sc[q][u] = u * RS + pw < rem ? sc[q][u] : -__builtin_inff();
             }
 #pragma unroll
             for (int q = 0; q < QG; ++q) {
