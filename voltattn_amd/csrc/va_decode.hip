@@ -131,10 +131,10 @@ __global__ __launch_bounds__(256) void decode_w1(DecodeArgs a) {
 #define VA_Q8_DEEP 1
 #endif
 #ifndef VA_Q4_WAVES
-#define VA_Q4_WAVES 4                // 4 waves x 4 rows
+#define VA_Q4_WAVES 4                // 4 waves x 2 rows
 #endif
 #ifndef VA_Q4_DEEP
-#define VA_Q4_DEEP 1
+#define VA_Q4_DEEP 0                 // 2 rows: L 4096 7.88 -> 7.58 us, 65536 49.0 -> 46.8 against 4
 #endif
 #ifndef VA_Q3_WAVES
 #define VA_Q3_WAVES 8                // 8 waves x 2 rows
