@@ -22,6 +22,11 @@ Method (reference bench, src/voltattn.cu:967-1070, re-derived for MI355X):
   * K/V are drawn N(0,1) on the GPU, quantized there (bit-exact quantizer) and
     replicated into enough copies to rotate a >= 2 GiB working set, so the
     MALL cannot serve the stream;
+  * settle: each row's buffers are created, then the host waits 500 ms
+    (--settle-ms) before any step of it runs: for ~100 ms after the previous
+    row's (or a probe's) multi-GiB buffers are freed, steps read 2-3.5 us slow
+    (q8+ L=16384: 25.3 against 23.4 us; measured on MI355X, not seen after a
+    0.5 s wait);
   * warm-up: untimed steps for >= 50 ms of wall time per row (--warm-ms), so
     the shader clock has ramped from its idle level, then W warm-up steps;
   * timed region: device synchronisation, one untimed lead step (so the start
@@ -155,6 +160,7 @@ def time_workload(va, w: Workload, steps: int, warmup: int, stream, steps_only: 
     first = lambda c: va.decode_splits(fmt, bufs[c % w.copies], H, L, D, S, G=G, stream=stream)
     e0, e1 = va.Event(), va.Event()
     try:
+        settle()
         # Residency pass: one untimed step on every rotated copy, so every timed
         # step finds its copy's address translations as warm as the others'
         # (first-touch page walks otherwise land in the first lap of the
@@ -246,10 +252,21 @@ def check_workload(va, w: Workload, heads) -> dict:
     return {"checked": ok, "check_heads": list(heads), "check_maxerr": worst}
 
 
+SETTLE_MS = 500.0     # --settle-ms
+
+
+def settle() -> None:
+    """Wait SETTLE_MS after a row's buffers are created (and earlier buffers
+    freed) before its first step: steps launched within ~100 ms of freeing a
+    multi-GiB buffer measured 2-3.5 us slow on MI355X."""
+    time.sleep(SETTLE_MS / 1e3)
+
+
 def time_fn(va, fn, copies: int, steps: int, warmup: int, stream) -> float:
     """Mean ms of `steps` back-to-back calls fn(copy, stream), rotating copies."""
     e0, e1 = va.Event(), va.Event()
     try:
+        settle()
         for c in range(copies):
             fn(c, stream)
         t_end = time.perf_counter() + 0.05  # clock warm-up, as in time_workload
@@ -445,6 +462,7 @@ CONFIG_ROWS = [
 
 
 def main() -> int:
+    global SETTLE_MS
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--gpus", type=int, default=1)
     # 100 steps keep the timed region of the longest row under 20 ms while the
@@ -462,6 +480,8 @@ def main() -> int:
     ap.add_argument("--splits", type=int, default=0, help="force S (0: va_pick_splits)")
     ap.add_argument("--warm-ms", type=float, default=50.0,
                     help="untimed steps for at least this long before each row's timed region")
+    ap.add_argument("--settle-ms", type=float, default=SETTLE_MS,
+                    help="wait after a row's buffers are created, before its first step")
     ap.add_argument("--probe-gib", type=float, default=4.0)
     ap.add_argument("--set-gib", type=float, default=2.0, help="rotated working set per row")
     ap.add_argument("--no-cpu", action="store_true")
@@ -475,6 +495,7 @@ def main() -> int:
                     help="first run one plain device-to-device copy of this many MiB "
                          "(calibrates rocprof FETCH_SIZE/WRITE_SIZE against known bytes)")
     args = ap.parse_args()
+    SETTLE_MS = args.settle_ms
 
     if args.gpus != 1:
         log(f"bench.py: --gpus {args.gpus} is not supported: this build measures one MI355X "
@@ -529,6 +550,7 @@ def main() -> int:
         nbytes = algo_bytes(fmt, H, L, D, G)
         gbs = nbytes / (t["mean_ms"] * 1e6)
         if nbytes not in sized:
+            settle()                 # the row's buffers were just freed
             sized[nbytes] = va.probe_read_sized(nbytes, int(args.set_gib * 2**30), launches=max(20, args.steps))
         sz_us, sz_gbs = sized[nbytes]
         r = {"config": cfg, "fmt": fmt.label, "L": L, "S": S,

@@ -6,7 +6,7 @@
 // lane, a 6-step cross-lane sum and an exact per-position online-softmax
 // update — the attribution control of the reference's attn_f16/q8/q4
 // (src/voltattn.cu:122-320).
-#include "va_tiled.hpp"
+#include "va_phased.hpp"
 
 #include <algorithm>
 
@@ -143,15 +143,74 @@ __global__ __launch_bounds__(256) void decode_w1(DecodeArgs a) {
 #define VA_Q3_DEEP 0
 #endif
 
+// Two-phase kernel (va_phased.hpp) per kind: VA_<KIND>_PHASED = 1 selects it
+// for the reference-shape launches, with VA_<KIND>_PU rows per lane per tile
+// of one tensor and VA_<KIND>_PWAVES waves per group. Interleaved A/B on one
+// MI355X, H=32 D=128 G=32, against the single-pass tiled kernel: q8+ L 16384
+// 24.36 -> 23.46 us, 65536 85.17 -> 80.65, 4096 9.19 -> 9.21; f16+ L 16384
+// 41.12 -> 40.54, 4096 13.24 -> 12.88. The codecs with more vector-ALU work
+// per byte lose with it (q4+ 65536 46.07 -> 50.00, q3+ 262144 150.1 -> 187.6
+// at 4 waves, 182.6 at 8), so they keep the tiled kernel.
+#ifndef VA_F16_PHASED
+#define VA_F16_PHASED 1
+#endif
+#ifndef VA_Q8_PHASED
+#define VA_Q8_PHASED 1
+#endif
+#ifndef VA_Q4_PHASED
+#define VA_Q4_PHASED 0
+#endif
+#ifndef VA_Q3_PHASED
+#define VA_Q3_PHASED 0
+#endif
+#ifndef VA_F16_PU
+#define VA_F16_PU 4
+#endif
+#ifndef VA_Q8_PU
+#define VA_Q8_PU 4
+#endif
+#ifndef VA_Q4_PU
+#define VA_Q4_PU 4
+#endif
+#ifndef VA_Q3_PU
+#define VA_Q3_PU 4
+#endif
+#ifndef VA_F16_PWAVES
+#define VA_F16_PWAVES 4
+#endif
+#ifndef VA_Q8_PWAVES
+#define VA_Q8_PWAVES 4
+#endif
+#ifndef VA_Q4_PWAVES
+#define VA_Q4_PWAVES 4
+#endif
+#ifndef VA_Q3_PWAVES
+#define VA_Q3_PWAVES 4
+#endif
+
 template <int KIND> struct TiledCfg;
-template <> struct TiledCfg<KF16> { static constexpr int waves = VA_F16_WAVES; static constexpr bool deep = VA_F16_DEEP; };
-template <> struct TiledCfg<KQ8>  { static constexpr int waves = VA_Q8_WAVES;  static constexpr bool deep = VA_Q8_DEEP;  };
-template <> struct TiledCfg<KQ4>  { static constexpr int waves = VA_Q4_WAVES;  static constexpr bool deep = VA_Q4_DEEP;  };
-template <> struct TiledCfg<KQ3>  { static constexpr int waves = VA_Q3_WAVES;  static constexpr bool deep = VA_Q3_DEEP;  };
+template <> struct TiledCfg<KF16> {
+    static constexpr int waves = VA_F16_WAVES; static constexpr bool deep = VA_F16_DEEP;
+    static constexpr bool phased = VA_F16_PHASED; static constexpr int pu = VA_F16_PU; static constexpr int pwaves = VA_F16_PWAVES;
+};
+template <> struct TiledCfg<KQ8> {
+    static constexpr int waves = VA_Q8_WAVES; static constexpr bool deep = VA_Q8_DEEP;
+    static constexpr bool phased = VA_Q8_PHASED; static constexpr int pu = VA_Q8_PU; static constexpr int pwaves = VA_Q8_PWAVES;
+};
+template <> struct TiledCfg<KQ4> {
+    static constexpr int waves = VA_Q4_WAVES; static constexpr bool deep = VA_Q4_DEEP;
+    static constexpr bool phased = VA_Q4_PHASED; static constexpr int pu = VA_Q4_PU; static constexpr int pwaves = VA_Q4_PWAVES;
+};
+template <> struct TiledCfg<KQ3> {
+    static constexpr int waves = VA_Q3_WAVES; static constexpr bool deep = VA_Q3_DEEP;
+    static constexpr bool phased = VA_Q3_PHASED; static constexpr int pu = VA_Q3_PU; static constexpr int pwaves = VA_Q3_PWAVES;
+};
 template <int KIND> struct TiledShape {
     static_assert(TiledCfg<KIND>::waves == 4 || TiledCfg<KIND>::waves == 8, "4 or 8 waves per group");
-    static constexpr int waves = TiledCfg<KIND>::waves;
-    static constexpr int U = TiledCfg<KIND>::deep ? UnrollSet<KIND>::b : UnrollSet<KIND>::a;
+    static constexpr bool phased = TiledCfg<KIND>::phased;
+    static constexpr int waves = phased ? TiledCfg<KIND>::pwaves : TiledCfg<KIND>::waves;
+    static constexpr int U = phased ? TiledCfg<KIND>::pu
+                                    : TiledCfg<KIND>::deep ? UnrollSet<KIND>::b : UnrollSet<KIND>::a;
 };
 
 template <int KIND, int D>
@@ -182,8 +241,12 @@ static hipError_t launch_one(bool tiled, int H, const DecodeArgs& a, hipStream_t
     const dim3 grid((unsigned)(H * a.S));
     if (tiled) {
         using T = TiledShape<KIND>;
-        hipLaunchKernelGGL((decode_tiled<KIND, D, G, T::U, T::waves, 1, false>), grid, dim3(T::waves * 64), 0, st,
-                           VA_TILED_ARGS(a));
+        if constexpr (T::phased)
+            hipLaunchKernelGGL((decode_phased<KIND, D, G, T::U, T::waves>), grid, dim3(T::waves * 64), 0, st,
+                               VA_TILED_ARGS(a));
+        else
+            hipLaunchKernelGGL((decode_tiled<KIND, D, G, T::U, T::waves, 1, false>), grid, dim3(T::waves * 64), 0, st,
+                               VA_TILED_ARGS(a));
     } else {
         if constexpr (KIND == KQ3) return hipErrorInvalidValue;
         else hipLaunchKernelGGL((decode_w1<KIND, D, G>), grid, dim3(256), 0, st, a);

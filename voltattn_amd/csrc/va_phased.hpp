@@ -1,0 +1,265 @@
+// va_phased.hpp — the two-phase split-L decode kernel of the reference shape
+// (one query head per K/V head, contiguous K/V): the same partials, splits,
+// codecs and merge as decode_tiled<..., QG = 1, PAGED = false>
+// (va_tiled.hpp), with the K and V rows of a split read in separate phases.
+//
+// A work-group walks its split in rounds of up to RT work-group tiles. Each
+// round first streams the K rows of its positions (with the K scales): every
+// row's raw score (q.k times the group scale) goes to the wave's slice of LDS
+// and the wave keeps its maximum. Then it streams the V rows of the same
+// positions (with the V scales): each lane reads back its row's score and
+// accumulates p = exp2(score * qs - m) against the row, m being the exact
+// maximum of the wave's scores so far (one rescale of l and o per round, where
+// it rises). Reference: src/voltattn.cu:364-649 (one pass over the position
+// that reads K and V together, an online softmax per position).
+//
+// Why two phases: a work-group that reads one stream at a time keeps half as
+// many DRAM streams open as one that reads K and V side by side. A read-only
+// kernel with the decode grid (one 4-wave group per CU, 16 KB per register
+// stage, two stages) measured on MI355X: 268 MB in 38.7 us as K-then-V phases
+// against 40.2 us as interleaved K and V loads at the same depth (40.6 us at
+// the 32 KB stages of the interleaved decode loop); 142.6 MB in 21.8 against
+// 21.9 (22.1) us.
+//
+// Each lane loads LB = 16 bytes (12 for q3) of a row per load, U loads per
+// tile of one tensor; the loads of a 4-wave group interleave by instruction
+// (load u of wave w reads rows u*PPW*WAVES + w*PPW ..), as in decode_tiled.
+// Two register stages alternate over the stage sequence K tiles 0..T-1, V
+// tiles 0..T-1 of round 0, then round 1, ...: the next stage's loads are in
+// flight while the current one is computed, across the phase change too.
+// Loads past the end of the split return zeros without memory traffic, which
+// covers the last, partial tile and the prefetch after the last stage.
+#pragma once
+#include "va_tiled.hpp"
+
+namespace va {
+
+// Positions per round of a work-group: 32 KB of scores in LDS.
+constexpr int PHASED_ROUND_ROWS = 8192;
+
+template <int KIND, int D, int G, int U, int WAVES>
+__global__ __launch_bounds__(WAVES * 64, 1) void decode_phased(
+    const uint8_t* k, const uint8_t* v, const uint16_t* sk, const uint16_t* sv,
+    int L_, int S_, int chunk_, int slot_, const uint16_t* q, void* dst, DecodeArgs rest) {
+    DecodeArgs a = rest;
+    a.k = k; a.v = v; a.sk = sk; a.sv = sv; a.q = q;
+    a.out = static_cast<uint16_t*>(dst);
+    a.ws = static_cast<float*>(dst);
+    a.L = L_; a.S = S_; a.chunk = chunk_; a.ticket_slot = slot_;
+    a.qscale = qscale_of<D>();
+    using T = Tile<KIND, D>;
+    using C = Codec<KIND>;
+    using LoadT = typename LaneLoad<KIND>::type;
+    constexpr int ROWB = T::ROWB, LB = T::LB, LP = T::LP, PPW = T::PPW, EPL = T::EPL, NP = C::NP;
+    static_assert(EPL == C::EPL, "codec width");
+    constexpr bool QUANT = KIND != KF16;
+    constexpr int NG  = D / G;                   // scale groups per row
+    constexpr int TW  = PPW * U;                 // rows per wave per tile
+    constexpr int TB  = TW * WAVES;              // rows per work-group tile
+    constexpr int RT  = PHASED_ROUND_ROWS / TB;  // work-group tiles per round
+    static_assert(RT >= 1 && RT * TB == PHASED_ROUND_ROWS, "whole tiles per round");
+    constexpr int SCN = QUANT ? TW * NG : 1;     // scale entries of one tensor per wave tile
+    constexpr int SCE = !QUANT ? 1 : NG >= 2 ? SCN / 2 : SCN;  // scale dwords (NG >= 2) or halves per wave tile
+    constexpr int SCR = (SCE + 63) / 64;         // scale loads per lane
+    constexpr bool IL = WAVES == 4;              // interleaved waves (as decode_tiled's contiguous 4-wave form)
+    constexpr int RS = IL ? PPW * WAVES : PPW;   // rows between a wave's loads
+    constexpr int WS = IL ? PPW : TW;            // rows between waves
+    constexpr int SPG = NG >= 2 ? PPW * NG / 2 : PPW;  // scale entries of one load's rows
+    static_assert(!QUANT || G % EPL == 0, "a lane's elements share one scale group");
+    static_assert(SCE % 64 == 0 || SCR == 1, "scale entries fill whole wave loads");
+
+    __shared__ uint32_t s_sc[WAVES][SCN];        // scale entries of the wave's current tile (low halves)
+    __shared__ float s_score[WAVES][RT * TW];              // raw scores of the wave's rows in the round
+
+    Route rt;
+    rt.mg  = (int)blockIdx.x / a.S;
+    rt.s   = (int)blockIdx.x - rt.mg * a.S;
+    rt.nq  = 1;
+    rt.oh0 = rt.mg;
+    const int hk = rt.mg, s = rt.s;
+    const unsigned epoch = read_epoch<1>(a, rt.mg);
+    const int wave = uniform((int)(threadIdx.x >> 6));
+    const int lane = (int)(threadIdx.x & 63);
+    const int sl   = lane % LP;                  // lane within its row
+    const int pw   = lane / LP;                  // row slot within a wave load
+    const int grp  = (sl * EPL) / G;             // scale group of this lane
+
+    const int j0 = s * a.chunk;
+    const int n  = min(a.L - j0, a.chunk);       // rows of this split (<= 0: empty)
+
+    float m[1] = {M_INIT}, l[1] = {0.f};
+    float o[1][EPL];
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) o[0][e] = 0.f;
+
+    if (n > 0) {
+        const uint32_t lane_off = (uint32_t)(pw * ROWB + sl * LB);
+        const int ntile = (n + TB - 1) / TB;     // work-group tiles of the split
+        const int nst   = 2 * ntile;             // stages: a K and a V pass over every tile
+        const size_t row0 = (size_t)hk * a.L + j0;
+        const __amdgpu_buffer_rsrc_t rk = make_rsrc(a.k + row0 * ROWB, (uint32_t)n * ROWB);
+        const __amdgpu_buffer_rsrc_t rv = make_rsrc(a.v + row0 * ROWB, (uint32_t)n * ROWB);
+        const __amdgpu_buffer_rsrc_t rsk = QUANT ? make_rsrc(a.sk + row0 * NG, (uint32_t)n * NG * 2) : rk;
+        const __amdgpu_buffer_rsrc_t rsv = QUANT ? make_rsrc(a.sv + row0 * NG, (uint32_t)n * NG * 2) : rv;
+
+        // Stage i -> (tile of the split, phase, tile within the round). Rounds
+        // before the last hold RT tiles.
+        struct StageAt { int tile; bool vph; int t; int tr; };
+        auto stage_at = [&](int i) {
+            StageAt x;
+            const int r  = i / (2 * RT);
+            const int w  = i - r * 2 * RT;
+            x.tr   = min(RT, ntile - r * RT);    // tiles of this round
+            x.vph  = w >= x.tr;
+            x.t    = x.vph ? w - x.tr : w;
+            x.tile = r * RT + x.t;
+            return x;
+        };
+
+        LoadT xa[U], xb[U];
+        uint32_t sa[SCR], sb[SCR];
+
+        // Issue order pinned (scales, then rows), as in decode_tiled, so every
+        // wait stays partial. A stage past the last one reads past the split's
+        // end (zeros, no memory access).
+        auto load_stage = [&](int i, LoadT* xx, uint32_t* ss) {
+            const StageAt st = stage_at(i);
+            const bool past = i >= nst;
+            const __amdgpu_buffer_rsrc_t tx = st.vph && !past ? rv : rk;
+            const __amdgpu_buffer_rsrc_t ts = st.vph && !past ? rsv : rsk;
+            const uint32_t t0 = past ? (uint32_t)n : (uint32_t)(st.tile * TB + wave * WS);
+            const uint32_t tpos = sgpr(t0);
+            __builtin_amdgcn_sched_barrier(0);
+            if constexpr (QUANT) {               // lanes past SCE repeat the last entry (unused)
+#pragma unroll
+                for (int r = 0; r < SCR; ++r) {
+                    const uint32_t sidx = (uint32_t)min(lane + 64 * r, SCE - 1);
+                    const uint32_t gap = (sidx / SPG) * (uint32_t)(RS - PPW) * NG * 2;   // bytes
+                    if constexpr (NG >= 2) ss[r] = ld32(ts, sidx * 4 + gap, tpos * NG * 2);
+                    else ss[r] = ld16(ts, sidx * 2 + gap, tpos * 2);
+                }
+            }
+#pragma unroll
+            for (int u = 0; u < U; ++u)
+                xx[u] = lane_load<KIND>(tx, lane_off + (uint32_t)(u * RS * ROWB), tpos * ROWB);
+            __builtin_amdgcn_sched_barrier(0);
+        };
+
+        load_stage(0, xa, sa);
+
+        typename C::QReg qr;
+        C::template load_q<LP>(qr, a.q + (size_t)rt.oh0 * D + sl * EPL, a.qscale);
+        const uint32_t magic = C::magic();
+
+        auto stage_scales = [&](const uint32_t* ss) {
+            if constexpr (QUANT) {
+#pragma unroll
+                for (int r = 0; r < SCR; ++r) {
+                    const int e = lane + 64 * r;
+                    if (e < SCE) {               // entry i in the low half of s_sc[wave][i]
+                        if constexpr (NG >= 2) {
+                            s_sc[wave][2 * e]     = ss[r];
+                            s_sc[wave][2 * e + 1] = ss[r] >> 16;
+                        } else {
+                            s_sc[wave][e] = ss[r];
+                        }
+                    }
+                }
+            }
+        };
+
+        // V offset window (va_tiled.hpp): vsum sums the weights ev since the
+        // last fix_v, which removes the stored codes' offset in bulk.
+        float vsum = 0.f;
+        auto fix_v = [&]() {
+            if constexpr (C::VFIX) {
+#pragma unroll
+                for (int e = 0; e < EPL; ++e) o[0][e] = __builtin_fmaf(vsum, C::voff(e), o[0][e]);
+                vsum = 0.f;
+            }
+        };
+
+        float lmax = -__builtin_inff();          // this lane's largest raw score of the round
+
+        // K phase of one tile: raw scores to LDS; rows past the split's end
+        // (the last tile only) score -inf.
+        auto score_tile = [&](auto masked, const StageAt& st, const LoadT* kk) {
+            constexpr bool MASK = decltype(masked)::value;
+            const int rem = MASK ? uniform(n - st.tile * TB - wave * WS) : 0;   // rows from the wave's first
+            uint32_t scl[U];                     // the rows' K scales, read before any score is stored
+#pragma unroll
+            for (int u = 0; u < U; ++u) scl[u] = QUANT ? s_sc[wave][(u * PPW + pw) * NG + grp] : 0u;
+            float sc[U];
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                h2 pk[NP];
+                C::unpack_k(kk[u], magic, pk);
+                float d = C::dot(pk, qr);
+                if constexpr (QUANT) d = mul_lo_h(d, scl[u]);
+                sc[u] = group_sum<LP>(d);
+                if constexpr (MASK) sc[u] = u * RS + pw < rem ? sc[u] : -__builtin_inff();
+                lmax = fmaxf(lmax, sc[u]);
+            }
+            // one lane per row stores its score: one branch per tile, so the
+            // rows above stay in one block and their chains interleave
+            if (sl == 0) {
+#pragma unroll
+                for (int u = 0; u < U; ++u) s_score[wave][st.t * TW + u * PPW + pw] = sc[u];
+            }
+            if (st.t == st.tr - 1) {             // the round's maximum; rescale where it rose
+                const float mn = fmaxf(m[0], uniformf(wave_max(lmax)) * qr.qs);
+                if (mn > m[0]) {
+                    const float c = fast_exp2(m[0] - mn);
+                    l[0] *= c;
+                    vsum *= c;
+#pragma unroll
+                    for (int e = 0; e < EPL; ++e) o[0][e] *= c;
+                    m[0] = mn;
+                }
+                lmax = -__builtin_inff();
+            }
+        };
+        // V phase of one tile.
+        auto value_tile = [&](const StageAt& st, const LoadT* vv) {
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                const int slot = u * PPW + pw;
+                const float sc = s_score[wave][st.t * TW + slot];
+                h2 pv[NP];
+                C::unpack_v(vv[u], pv);
+                const float p = fast_exp2(__builtin_fmaf(sc, qr.qs, -m[0]));
+                l[0] += p;
+                float ev = p;
+                if constexpr (QUANT) ev = mul_lo_h(p, s_sc[wave][slot * NG + grp]);
+                if constexpr (C::VFIX) vsum += ev;
+                C::axpy_v(pv, ev, o[0]);
+            }
+        };
+        auto compute = [&](int i, const LoadT* xx) {
+            const StageAt st = stage_at(i);
+            if (st.vph) {
+                value_tile(st, xx);
+            } else if (st.tile == ntile - 1) {
+                score_tile(std::true_type{}, st, xx);
+            } else {
+                score_tile(std::false_type{}, st, xx);
+            }
+        };
+
+        // nst is even: the stages run in (A, B) pairs with no tail.
+        for (int i = 0; i < nst; i += 2) {
+            stage_scales(sa);
+            load_stage(i + 1, xb, sb);
+            compute(i, xa);
+            stage_scales(sb);
+            load_stage(i + 2, xa, sa);
+            compute(i + 1, xb);
+            if (stage_at(i + 1).vph) fix_v();    // <= 2U rows per lane since the last fix
+        }
+        fix_finish<C>(o[0], vsum, std::make_integer_sequence<int, EPL>{});
+    }
+
+    group_finish<D, LP, EPL, WAVES, 1, false>(a, rt, m, l, o, false, epoch);
+}
+
+} // namespace va

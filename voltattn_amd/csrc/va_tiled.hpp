@@ -81,6 +81,119 @@ __device__ __forceinline__ void fix_finish(float* o, float s, std::integer_seque
     (fix_finish_one<C, E>(o[E], s), ...);
 }
 
+// End of a split-L work-group: the per-lane state of every wave (m[q] wave-
+// uniform, in log2 units; l[q] and o[q][EPL] over the lane's rows, l repeated
+// on the LP lanes of a row) is folded into one partial (M, l, o[D]) per query
+// slot — the slots of a DPP row first, then rows and waves via LDS — and
+// handed to finish_partial. A paged tile with a bad page id in any wave
+// (`bad`) marks every partial of the group (l = NaN).
+template <int D, int LP, int EPL, int WAVES, int QG, bool PAGED>
+__device__ __forceinline__ void group_finish(const DecodeArgs& a, const Route& rt, const float (&m)[QG],
+                                             float (&l)[QG], float (&o)[QG][EPL], bool bad, unsigned epoch) {
+    __shared__ float s_red[QG][WAVES * 4][D + 1];
+    __shared__ float s_l[QG][WAVES];
+    __shared__ float s_m[QG][WAVES];
+    const int wave = uniform((int)(threadIdx.x >> 6));
+    const int lane = (int)(threadIdx.x & 63);
+    const int sl   = lane % LP;
+#pragma unroll
+    for (int q = 0; q < QG; ++q) {
+#pragma unroll
+        for (int off = LP; off < 16; off *= 2) {
+            if (off == 1) { l[q] += dpp<dpp_row_ror(1)>(l[q]); for (int e = 0; e < EPL; ++e) o[q][e] += dpp<dpp_row_ror(1)>(o[q][e]); }
+            if (off == 2) { l[q] += dpp<dpp_row_ror(2)>(l[q]); for (int e = 0; e < EPL; ++e) o[q][e] += dpp<dpp_row_ror(2)>(o[q][e]); }
+            if (off == 4) { l[q] += dpp<dpp_row_ror(4)>(l[q]); for (int e = 0; e < EPL; ++e) o[q][e] += dpp<dpp_row_ror(4)>(o[q][e]); }
+            if (off == 8) { l[q] += dpp<dpp_row_ror(8)>(l[q]); for (int e = 0; e < EPL; ++e) o[q][e] += dpp<dpp_row_ror(8)>(o[q][e]); }
+        }
+        // The sums are used only by the lanes that write them out; computed
+        // here in every lane, each add stays one DPP instruction (sunk into
+        // the write-out branch it would be a DPP move plus an add).
+        asm volatile("" : "+v"(l[q]));
+#pragma unroll
+        for (int e = 0; e < EPL; ++e) asm volatile("" : "+v"(o[q][e]));
+    }
+    const int row = lane >> 4;
+    if ((lane & 15) < LP) {                       // one slot per 16-lane row holds the row sum
+#pragma unroll
+        for (int q = 0; q < QG; ++q) {
+#pragma unroll
+            for (int e = 0; e < EPL; ++e) s_red[q][wave * 4 + row][sl * EPL + e] = o[q][e];
+        }
+    }
+    // l: every lane holds its row's sum; the rows are summed in the wave (row
+    // swaps), so the fold below takes one l per wave.
+    float lw[QG];
+#pragma unroll
+    for (int q = 0; q < QG; ++q) lw[q] = rows_sum(l[q]);
+    if (lane == 0) {
+#pragma unroll
+        for (int q = 0; q < QG; ++q) {
+            s_m[q][wave] = m[q];
+            s_l[q][wave] = lw[q];
+        }
+    }
+    // A bad tile in any wave marks every partial of the group (l = NaN).
+    bool any_bad = false;
+    if constexpr (PAGED) any_bad = __syncthreads_or(bad);
+    else __syncthreads();
+    const int t = (int)threadIdx.x;
+    float M[QG], acc[QG], ls[QG];
+    if constexpr (QG < 4) {
+        // threads t < D fold every query slot of dimension t (measured faster
+        // than the all-thread fold below up to two slots)
+#pragma unroll
+        for (int q = 0; q < QG; ++q) {
+            M[q] = 0.f;
+            acc[q] = 0.f;
+            ls[q] = 0.f;
+            if (t < D) {
+                M[q] = s_m[q][0];
+#pragma unroll
+                for (int w = 1; w < WAVES; ++w) M[q] = fmaxf(M[q], s_m[q][w]);
+                float f[WAVES];
+#pragma unroll
+                for (int w = 0; w < WAVES; ++w) f[w] = fast_exp2(s_m[q][w] - M[q]);
+#pragma unroll
+                for (int r = 0; r < WAVES * 4; ++r) acc[q] = __builtin_fmaf(f[r / 4], s_red[q][r][t], acc[q]);
+#pragma unroll
+                for (int w = 0; w < WAVES; ++w) ls[q] = __builtin_fmaf(f[w], s_l[q][w], ls[q]);
+                if (any_bad) ls[q] = __builtin_nanf("");
+            }
+        }
+    } else {
+        // four query slots: every thread folds (query slot, dimension) pairs
+        __shared__ float s_acc[QG][D];
+        __shared__ float s_mf[QG], s_lf[QG];
+        for (int i = t; i < QG * D; i += WAVES * 64) {
+            const int q = i / D, d = i - (i / D) * D;
+            float m = s_m[q][0];
+#pragma unroll
+            for (int w = 1; w < WAVES; ++w) m = fmaxf(m, s_m[q][w]);
+            float f[WAVES];
+#pragma unroll
+            for (int w = 0; w < WAVES; ++w) f[w] = fast_exp2(s_m[q][w] - m);
+            float sacc = 0.f, sl = 0.f;
+#pragma unroll
+            for (int r = 0; r < WAVES * 4; ++r) sacc = __builtin_fmaf(f[r / 4], s_red[q][r][d], sacc);
+            s_acc[q][d] = sacc;
+            if (d == 0) {
+#pragma unroll
+                for (int w = 0; w < WAVES; ++w) sl = __builtin_fmaf(f[w], s_l[q][w], sl);
+                s_mf[q] = m;
+                s_lf[q] = any_bad ? __builtin_nanf("") : sl;
+            }
+        }
+        __syncthreads();
+#pragma unroll
+        for (int q = 0; q < QG; ++q) {
+            M[q] = s_mf[q];
+            ls[q] = s_lf[q];
+            acc[q] = t < D ? s_acc[q][t] : 0.f;
+        }
+    }
+    finish_partial<D, WAVES * 64, QG>(a, rt, M, ls, acc, epoch);
+}
+
 template <int KIND, int D, int G, int U, int WAVES, int QG, bool PAGED, int MINB = 1>
 __global__ __launch_bounds__(WAVES * 64, MINB) void decode_tiled(
     const uint8_t* k, const uint8_t* v, const uint16_t* sk, const uint16_t* sv,
@@ -119,9 +232,6 @@ __global__ __launch_bounds__(WAVES * 64, MINB) void decode_tiled(
     static_assert(SCE % 64 == 0 || SCR == 1, "scale entries fill whole wave loads");
 
     __shared__ uint32_t s_scale[WAVES][SCN];
-    __shared__ float    s_red[QG][WAVES * 4][D + 1];
-    __shared__ float    s_l[QG][WAVES];
-    __shared__ float    s_m[QG][WAVES];
     __shared__ int      s_page[PAGED ? MAX_SPLIT_PAGES : 1];
 
     // ---- work-group -> (sequence b, KV head hk, query sub-group, split s)
@@ -430,103 +540,7 @@ __global__ __launch_bounds__(WAVES * 64, MINB) void decode_tiled(
         for (int q = 0; q < QG; ++q) fix_finish<C>(o[q], S[q], std::make_integer_sequence<int, EPL>{});
     }
 
-    // ---- work-group merge: slots of a DPP row first, then rows/waves via LDS.
-#pragma unroll
-    for (int q = 0; q < QG; ++q) {
-#pragma unroll
-        for (int off = LP; off < 16; off *= 2) {
-            if (off == 1) { l[q] += dpp<dpp_row_ror(1)>(l[q]); for (int e = 0; e < EPL; ++e) o[q][e] += dpp<dpp_row_ror(1)>(o[q][e]); }
-            if (off == 2) { l[q] += dpp<dpp_row_ror(2)>(l[q]); for (int e = 0; e < EPL; ++e) o[q][e] += dpp<dpp_row_ror(2)>(o[q][e]); }
-            if (off == 4) { l[q] += dpp<dpp_row_ror(4)>(l[q]); for (int e = 0; e < EPL; ++e) o[q][e] += dpp<dpp_row_ror(4)>(o[q][e]); }
-            if (off == 8) { l[q] += dpp<dpp_row_ror(8)>(l[q]); for (int e = 0; e < EPL; ++e) o[q][e] += dpp<dpp_row_ror(8)>(o[q][e]); }
-        }
-        // The sums are used only by the lanes that write them out; computed
-        // here in every lane, each add stays one DPP instruction (sunk into
-        // the write-out branch it would be a DPP move plus an add).
-        asm volatile("" : "+v"(l[q]));
-#pragma unroll
-        for (int e = 0; e < EPL; ++e) asm volatile("" : "+v"(o[q][e]));
-    }
-    const int row = lane >> 4;
-    if ((lane & 15) < LP) {                       // one slot per 16-lane row holds the row sum
-#pragma unroll
-        for (int q = 0; q < QG; ++q) {
-#pragma unroll
-            for (int e = 0; e < EPL; ++e) s_red[q][wave * 4 + row][sl * EPL + e] = o[q][e];
-        }
-    }
-    // l: every lane holds its row's sum; the rows are summed in the wave (row
-    // swaps), so the fold below takes one l per wave.
-    float lw[QG];
-#pragma unroll
-    for (int q = 0; q < QG; ++q) lw[q] = rows_sum(l[q]);
-    if (lane == 0) {
-#pragma unroll
-        for (int q = 0; q < QG; ++q) {
-            s_m[q][wave] = m[q];
-            s_l[q][wave] = lw[q];
-        }
-    }
-    // A bad tile in any wave marks every partial of the group (l = NaN).
-    bool any_bad = false;
-    if constexpr (PAGED) any_bad = __syncthreads_or(bad);
-    else __syncthreads();
-    const int t = (int)threadIdx.x;
-    float M[QG], acc[QG], ls[QG];
-    if constexpr (QG < 4) {
-        // threads t < D fold every query slot of dimension t (measured faster
-        // than the all-thread fold below up to two slots)
-#pragma unroll
-        for (int q = 0; q < QG; ++q) {
-            M[q] = 0.f;
-            acc[q] = 0.f;
-            ls[q] = 0.f;
-            if (t < D) {
-                M[q] = s_m[q][0];
-#pragma unroll
-                for (int w = 1; w < WAVES; ++w) M[q] = fmaxf(M[q], s_m[q][w]);
-                float f[WAVES];
-#pragma unroll
-                for (int w = 0; w < WAVES; ++w) f[w] = fast_exp2(s_m[q][w] - M[q]);
-#pragma unroll
-                for (int r = 0; r < WAVES * 4; ++r) acc[q] = __builtin_fmaf(f[r / 4], s_red[q][r][t], acc[q]);
-#pragma unroll
-                for (int w = 0; w < WAVES; ++w) ls[q] = __builtin_fmaf(f[w], s_l[q][w], ls[q]);
-                if (any_bad) ls[q] = __builtin_nanf("");
-            }
-        }
-    } else {
-        // four query slots: every thread folds (query slot, dimension) pairs
-        __shared__ float s_acc[QG][D];
-        __shared__ float s_mf[QG], s_lf[QG];
-        for (int i = t; i < QG * D; i += WAVES * 64) {
-            const int q = i / D, d = i - (i / D) * D;
-            float m = s_m[q][0];
-#pragma unroll
-            for (int w = 1; w < WAVES; ++w) m = fmaxf(m, s_m[q][w]);
-            float f[WAVES];
-#pragma unroll
-            for (int w = 0; w < WAVES; ++w) f[w] = fast_exp2(s_m[q][w] - m);
-            float sacc = 0.f, sl = 0.f;
-#pragma unroll
-            for (int r = 0; r < WAVES * 4; ++r) sacc = __builtin_fmaf(f[r / 4], s_red[q][r][d], sacc);
-            s_acc[q][d] = sacc;
-            if (d == 0) {
-#pragma unroll
-                for (int w = 0; w < WAVES; ++w) sl = __builtin_fmaf(f[w], s_l[q][w], sl);
-                s_mf[q] = m;
-                s_lf[q] = any_bad ? __builtin_nanf("") : sl;
-            }
-        }
-        __syncthreads();
-#pragma unroll
-        for (int q = 0; q < QG; ++q) {
-            M[q] = s_mf[q];
-            ls[q] = s_lf[q];
-            acc[q] = t < D ? s_acc[q][t] : 0.f;
-        }
-    }
-    finish_partial<D, WAVES * 64, QG>(a, rt, M, ls, acc, epoch);
+    group_finish<D, LP, EPL, WAVES, QG, PAGED>(a, rt, m, l, o, bad, epoch);
 }
 
 } // namespace va
