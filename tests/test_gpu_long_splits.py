@@ -50,3 +50,26 @@ def test_long_split_partials(shape):
             lse2 = m + math.log2(l)
             assert abs(lse2 - lse[h, s] / math.log(2.0)) <= 2e-5 * (1 + abs(lse2)), (h, s)
             np.testing.assert_allclose(o / l, avg[h, s], rtol=2e-5, atol=2e-6)
+
+
+# Splits of more than one round of the two-phase kernel (8192 positions of K,
+# then of V, per round; va_phased.hpp), f16+ and q8+: a ragged last round, a
+# round of a single work-group tile (its K and V stages share one register
+# pair), and a split whose last round holds one position.
+ROUND_SHAPES = [("f16+", 16, 2, 40000, 128, 3, 64),    # chunk 13334: 8192 + 5142
+                ("q8+", 8, 2, 65541, 128, 4, 32),      # chunk 16386: 8192 + 8192 + 2
+                ("f16+", 16, 1, 16385, 64, 1, 64),     # one split: 8192 + 8192 + 1
+                ("q8+", 8, 1, 24577, 128, 1, 64)]      # one split: 3 rounds + 1 position
+
+
+@pytest.mark.parametrize("shape", ROUND_SHAPES, ids=lambda s: "{}-H{}-L{}-D{}-S{}-G{}".format(s[0], *s[2:]))
+def test_multi_round_decode(shape):
+    name, bits, H, L, D, S, G = shape
+    c = gpu_util.case(bits, H, L, D, G, 0x30C5 ^ (H * 131 + L * 7 + D + S + G))
+    print(f"case {name} H={H} L={L} D={D} S={S} G={G} chunk={va.split_chunk(L, S)}", flush=True)
+    got = gpu_util.run_case(va.Fmt.parse(name), c, S)["out"].reshape(H, D)
+    ref = c["ref"].astype(np.float64).reshape(H, D)
+    ok, maxerr = oracle.gate(got.ravel(), ref.ravel())
+    assert ok, f"reference gate failed, maxerr={maxerr:.3e}"
+    bound = tight_bound(ref)
+    assert np.all(np.abs(got - ref) <= bound), float(np.max(np.abs(got - ref) / bound))
