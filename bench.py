@@ -254,6 +254,9 @@ def check_workload(va, w: Workload, heads) -> dict:
 
 SETTLE_MS = 500.0     # --settle-ms
 
+# The reference-shape kernel each "+" format runs (va_decode.hip: VA_<KIND>_PHASED).
+HEADLINE_KERNEL = {"f16+": "decode_phased", "q8+": "decode_phased", "q4+": "decode_tiled", "q3+": "decode_tiled"}
+
 
 def settle() -> None:
     """Wait SETTLE_MS after a row's buffers are created (and earlier buffers
@@ -609,7 +612,8 @@ def main() -> int:
     step_gbs = head["gbps"]
     roofline = {"bound": "hbm", "achieved": step_gbs, "peak": PEAK_HBM_GBPS, "unit": "GB/s",
                 "frac": step_gbs / PEAK_HBM_GBPS, "traffic": load_traffic(f"{args.headline}_L{args.L}_G{G}"),
-                "kernel": f"decode_tiled<{args.headline}> fused (split-L pass + LSE merge, one launch per step)",
+                "kernel": f"{HEADLINE_KERNEL.get(args.headline, 'decode_tiled')}<{args.headline}> fused "
+                          "(split-L pass + LSE merge, one launch per step)",
                 "algorithmic_bytes_per_launch": head["bytes"],
                 "kernel_ms": head["ms"], "frac_of_probed": step_gbs / ceiling,
                 "frac_of_sized_read": head["mbu_sized"], "sized_read_us": head["sized_ceiling_us"],
