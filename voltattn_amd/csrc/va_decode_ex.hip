@@ -9,7 +9,7 @@
 // of QG masks the spare slots. Grouped work-groups are 8 waves (two per SIMD)
 // where that fits in 256 VGPRs, else 4; the tile depth U shrinks as QG grows
 // so the two register stages of K/V loads still fit.
-#include "va_tiled.hpp"
+#include "va_phased.hpp"
 #include "va_mfma.hpp"
 
 #include <algorithm>
@@ -128,9 +128,29 @@ int tile_positions_ex(int kind, int D) {
     }
 }
 
+// Grouped-query f16 over contiguous K/V: the two-phase kernel (va_phased.hpp)
+// with QG query slots, one 8-wave group per CU (U = 4: 32 KB per stage);
+// VA_EX_PHASED = 0 keeps it on decode_tiled. Interleaved A/B on MI355X, Hq 32 /
+// Hkv 8, D 128, against decode_tiled: L 65536 48.40 -> 45.49 us, 16384 19.19 ->
+// 17.71, 4096 11.94 -> 11.58; 4-wave groups lost at short L (their merge of
+// four query slots runs on half the waves: 4096 11.89 -> 12.18).
+#ifndef VA_EX_PHASED
+#define VA_EX_PHASED 1
+#endif
+#ifndef VA_EX_PH_WAVES
+#define VA_EX_PH_WAVES 8
+#endif
+#ifndef VA_EX_PH_U
+#define VA_EX_PH_U 4
+#endif
+
 template <int KIND, int D, int G, int QG, bool PAGED>
 static hipError_t launch_ex(int groups, const DecodeArgs& a, hipStream_t st) {
-    if constexpr (mfma_kind_c<KIND, D> && QG >= 2) {
+    if constexpr (VA_EX_PHASED && KIND == KF16 && !PAGED && QG >= 2) {
+        hipLaunchKernelGGL((decode_phased<KIND, D, G, VA_EX_PH_U, VA_EX_PH_WAVES, QG>), dim3((unsigned)(groups * a.S)),
+                           dim3(VA_EX_PH_WAVES * 64), 0, st, VA_TILED_ARGS(a));
+        return hipGetLastError();
+    } else if constexpr (mfma_kind_c<KIND, D> && QG >= 2) {
         hipLaunchKernelGGL((decode_mfma<KIND, D, G, MFMA_WAVES, QG, PAGED>),
                            dim3((unsigned)(groups * a.S)), dim3(MFMA_WAVES * 64), 0, st, a);
         return hipGetLastError();

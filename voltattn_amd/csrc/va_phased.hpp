@@ -1,12 +1,14 @@
-// va_phased.hpp — the two-phase split-L decode kernel of the reference shape
-// (one query head per K/V head, contiguous K/V): the same partials, splits,
-// codecs and merge as decode_tiled<..., QG = 1, PAGED = false>
-// (va_tiled.hpp), with the K and V rows of a split read in separate phases.
+// va_phased.hpp — the two-phase split-L decode kernel over contiguous K/V:
+// the reference shape (one query head per K/V head, QG = 1) and grouped-query
+// decode of one sequence (QG query heads of a K/V head per work-group). The
+// same partials, splits, codecs and merge as decode_tiled<..., QG, PAGED =
+// false> (va_tiled.hpp), with the K and V rows of a split read in separate
+// phases.
 //
 // A work-group walks its split in rounds of up to RT work-group tiles. Each
 // round first streams the K rows of its positions (with the K scales): every
-// row's raw score (q.k times the group scale) goes to the wave's slice of LDS
-// and the wave keeps its maximum. Then it streams the V rows of the same
+// row's raw score (q.k times the group scale) for each of the QG query heads
+// goes to the wave's slice of LDS and the wave keeps each head's maximum. Then it streams the V rows of the same
 // positions (with the V scales): each lane reads back its row's score and
 // accumulates p = exp2(score * qs - m) against the row, m being the exact
 // maximum of the wave's scores so far (one rescale of l and o per round, where
@@ -34,10 +36,11 @@
 
 namespace va {
 
-// Positions per round of a work-group: 32 KB of scores in LDS.
+// Positions per round of a work-group: 32 KB of scores in LDS per query slot
+// at QG = 1, the same 32 KB split over the slots at QG > 1.
 constexpr int PHASED_ROUND_ROWS = 8192;
 
-template <int KIND, int D, int G, int U, int WAVES>
+template <int KIND, int D, int G, int U, int WAVES, int QG = 1>
 __global__ __launch_bounds__(WAVES * 64, 1) void decode_phased(
     const uint8_t* k, const uint8_t* v, const uint16_t* sk, const uint16_t* sv,
     int L_, int S_, int chunk_, int slot_, const uint16_t* q, void* dst, DecodeArgs rest) {
@@ -56,8 +59,8 @@ __global__ __launch_bounds__(WAVES * 64, 1) void decode_phased(
     constexpr int NG  = D / G;                   // scale groups per row
     constexpr int TW  = PPW * U;                 // rows per wave per tile
     constexpr int TB  = TW * WAVES;              // rows per work-group tile
-    constexpr int RT  = PHASED_ROUND_ROWS / TB;  // work-group tiles per round
-    static_assert(RT >= 1 && RT * TB == PHASED_ROUND_ROWS, "whole tiles per round");
+    constexpr int RT  = PHASED_ROUND_ROWS / QG / TB;   // work-group tiles per round
+    static_assert(RT >= 1 && RT * TB * QG == PHASED_ROUND_ROWS, "whole tiles per round");
     constexpr int SCN = QUANT ? TW * NG : 1;     // scale entries of one tensor per wave tile
     constexpr int SCE = !QUANT ? 1 : NG >= 2 ? SCN / 2 : SCN;  // scale dwords (NG >= 2) or halves per wave tile
     constexpr int SCR = (SCE + 63) / 64;         // scale loads per lane
@@ -69,15 +72,24 @@ __global__ __launch_bounds__(WAVES * 64, 1) void decode_phased(
     static_assert(SCE % 64 == 0 || SCR == 1, "scale entries fill whole wave loads");
 
     __shared__ uint32_t s_sc[WAVES][SCN];        // scale entries of the wave's current tile (low halves)
-    __shared__ float s_score[WAVES][RT * TW];              // raw scores of the wave's rows in the round
+    __shared__ float s_score[WAVES][QG][RT * TW];  // raw scores of the wave's rows in the round
 
+    // work-group -> (KV head hk, query sub-group, split s)
     Route rt;
     rt.mg  = (int)blockIdx.x / a.S;
     rt.s   = (int)blockIdx.x - rt.mg * a.S;
-    rt.nq  = 1;
-    rt.oh0 = rt.mg;
-    const int hk = rt.mg, s = rt.s;
-    const unsigned epoch = read_epoch<1>(a, rt.mg);
+    int hk = rt.mg;
+    if constexpr (QG == 1) {                     // the reference's shape: head = merge group
+        rt.nq  = 1;
+        rt.oh0 = rt.mg;
+    } else {                                     // one sequence: merge group = (hk, sub-group)
+        const int sub = rt.mg % a.nsub;
+        hk = (rt.mg / a.nsub) % a.hkv;
+        rt.nq  = min(QG, a.qgroup - sub * QG);
+        rt.oh0 = hk * a.qgroup + sub * QG;
+    }
+    const int s = rt.s;
+    const unsigned epoch = read_epoch<QG>(a, rt.mg);
     const int wave = uniform((int)(threadIdx.x >> 6));
     const int lane = (int)(threadIdx.x & 63);
     const int sl   = lane % LP;                  // lane within its row
@@ -87,10 +99,15 @@ __global__ __launch_bounds__(WAVES * 64, 1) void decode_phased(
     const int j0 = s * a.chunk;
     const int n  = min(a.L - j0, a.chunk);       // rows of this split (<= 0: empty)
 
-    float m[1] = {M_INIT}, l[1] = {0.f};
-    float o[1][EPL];
+    float m[QG], l[QG];
+    float o[QG][EPL];
 #pragma unroll
-    for (int e = 0; e < EPL; ++e) o[0][e] = 0.f;
+    for (int q = 0; q < QG; ++q) {
+        m[q] = M_INIT;
+        l[q] = 0.f;
+#pragma unroll
+        for (int e = 0; e < EPL; ++e) o[q][e] = 0.f;
+    }
 
     if (n > 0) {
         const uint32_t lane_off = (uint32_t)(pw * ROWB + sl * LB);
@@ -145,8 +162,12 @@ __global__ __launch_bounds__(WAVES * 64, 1) void decode_phased(
 
         load_stage(0, xa, sa);
 
-        typename C::QReg qr;
-        C::template load_q<LP>(qr, a.q + (size_t)rt.oh0 * D + sl * EPL, a.qscale);
+        // q slices of this lane (dims [sl*EPL, sl*EPL + EPL)); query slots past
+        // nq read query slot 0 (their results are dropped)
+        typename C::QReg qr[QG];
+#pragma unroll
+        for (int q = 0; q < QG; ++q)
+            C::template load_q<LP>(qr[q], a.q + (size_t)(rt.oh0 + (q < rt.nq ? q : 0)) * D + sl * EPL, a.qscale);
         const uint32_t magic = C::magic();
 
         auto stage_scales = [&](const uint32_t* ss) {
@@ -168,16 +189,23 @@ __global__ __launch_bounds__(WAVES * 64, 1) void decode_phased(
 
         // V offset window (va_tiled.hpp): vsum sums the weights ev since the
         // last fix_v, which removes the stored codes' offset in bulk.
-        float vsum = 0.f;
+        float vsum[QG];
+#pragma unroll
+        for (int q = 0; q < QG; ++q) vsum[q] = 0.f;
         auto fix_v = [&]() {
             if constexpr (C::VFIX) {
 #pragma unroll
-                for (int e = 0; e < EPL; ++e) o[0][e] = __builtin_fmaf(vsum, C::voff(e), o[0][e]);
-                vsum = 0.f;
+                for (int q = 0; q < QG; ++q) {
+#pragma unroll
+                    for (int e = 0; e < EPL; ++e) o[q][e] = __builtin_fmaf(vsum[q], C::voff(e), o[q][e]);
+                    vsum[q] = 0.f;
+                }
             }
         };
 
-        float lmax = -__builtin_inff();          // this lane's largest raw score of the round
+        float lmax[QG];                          // this lane's largest raw score of the round, per slot
+#pragma unroll
+        for (int q = 0; q < QG; ++q) lmax[q] = -__builtin_inff();
 
         // K phase of one tile: raw scores to LDS; rows past the split's end
         // (the last tile only) score -inf.
@@ -187,34 +215,42 @@ __global__ __launch_bounds__(WAVES * 64, 1) void decode_phased(
             uint32_t scl[U];                     // the rows' K scales, read before any score is stored
 #pragma unroll
             for (int u = 0; u < U; ++u) scl[u] = QUANT ? s_sc[wave][(u * PPW + pw) * NG + grp] : 0u;
-            float sc[U];
+            float sc[QG][U];
 #pragma unroll
             for (int u = 0; u < U; ++u) {
                 h2 pk[NP];
-                C::unpack_k(kk[u], magic, pk);
-                float d = C::dot(pk, qr);
-                if constexpr (QUANT) d = mul_lo_h(d, scl[u]);
-                sc[u] = group_sum<LP>(d);
-                if constexpr (MASK) sc[u] = u * RS + pw < rem ? sc[u] : -__builtin_inff();
-                lmax = fmaxf(lmax, sc[u]);
+                C::unpack_k(kk[u], magic, pk);  // once for every query slot
+#pragma unroll
+                for (int q = 0; q < QG; ++q) {
+                    float d = C::dot(pk, qr[q]);
+                    if constexpr (QUANT) d = mul_lo_h(d, scl[u]);
+                    sc[q][u] = group_sum<LP>(d);
+                    if constexpr (MASK) sc[q][u] = u * RS + pw < rem ? sc[q][u] : -__builtin_inff();
+                    lmax[q] = fmaxf(lmax[q], sc[q][u]);
+                }
             }
-            // one lane per row stores its score: one branch per tile, so the
+            // one lane per row stores its scores: one branch per tile, so the
             // rows above stay in one block and their chains interleave
             if (sl == 0) {
 #pragma unroll
-                for (int u = 0; u < U; ++u) s_score[wave][st.t * TW + u * PPW + pw] = sc[u];
-            }
-            if (st.t == st.tr - 1) {             // the round's maximum; rescale where it rose
-                const float mn = fmaxf(m[0], uniformf(wave_max(lmax)) * qr.qs);
-                if (mn > m[0]) {
-                    const float c = fast_exp2(m[0] - mn);
-                    l[0] *= c;
-                    vsum *= c;
+                for (int q = 0; q < QG; ++q)
 #pragma unroll
-                    for (int e = 0; e < EPL; ++e) o[0][e] *= c;
-                    m[0] = mn;
+                    for (int u = 0; u < U; ++u) s_score[wave][q][st.t * TW + u * PPW + pw] = sc[q][u];
+            }
+            if (st.t == st.tr - 1) {             // the round's maxima; rescale where one rose
+#pragma unroll
+                for (int q = 0; q < QG; ++q) {
+                    const float mn = fmaxf(m[q], uniformf(wave_max(lmax[q])) * qr[q].qs);
+                    if (mn > m[q]) {
+                        const float c = fast_exp2(m[q] - mn);
+                        l[q] *= c;
+                        vsum[q] *= c;
+#pragma unroll
+                        for (int e = 0; e < EPL; ++e) o[q][e] *= c;
+                        m[q] = mn;
+                    }
+                    lmax[q] = -__builtin_inff();
                 }
-                lmax = -__builtin_inff();
             }
         };
         // V phase of one tile.
@@ -222,15 +258,20 @@ __global__ __launch_bounds__(WAVES * 64, 1) void decode_phased(
 #pragma unroll
             for (int u = 0; u < U; ++u) {
                 const int slot = u * PPW + pw;
-                const float sc = s_score[wave][st.t * TW + slot];
                 h2 pv[NP];
-                C::unpack_v(vv[u], pv);
-                const float p = fast_exp2(__builtin_fmaf(sc, qr.qs, -m[0]));
-                l[0] += p;
-                float ev = p;
-                if constexpr (QUANT) ev = mul_lo_h(p, s_sc[wave][slot * NG + grp]);
-                if constexpr (C::VFIX) vsum += ev;
-                C::axpy_v(pv, ev, o[0]);
+                C::unpack_v(vv[u], pv);         // once for every query slot
+                uint32_t vsc = 0;
+                if constexpr (QUANT) vsc = s_sc[wave][slot * NG + grp];
+#pragma unroll
+                for (int q = 0; q < QG; ++q) {
+                    const float sc = s_score[wave][q][st.t * TW + slot];
+                    const float p = fast_exp2(__builtin_fmaf(sc, qr[q].qs, -m[q]));
+                    l[q] += p;
+                    float ev = p;
+                    if constexpr (QUANT) ev = mul_lo_h(p, vsc);
+                    if constexpr (C::VFIX) vsum[q] += ev;
+                    C::axpy_v(pv, ev, o[q]);
+                }
             }
         };
         auto compute = [&](int i, const LoadT* xx) {
@@ -264,10 +305,11 @@ __global__ __launch_bounds__(WAVES * 64, 1) void decode_phased(
         stage_scales(sb);
         compute(i + 1, xb);
         fix_v();
-        fix_finish<C>(o[0], vsum, std::make_integer_sequence<int, EPL>{});
+#pragma unroll
+        for (int q = 0; q < QG; ++q) fix_finish<C>(o[q], vsum[q], std::make_integer_sequence<int, EPL>{});
     }
 
-    group_finish<D, LP, EPL, WAVES, 1, false>(a, rt, m, l, o, false, epoch);
+    group_finish<D, LP, EPL, WAVES, QG, false>(a, rt, m, l, o, false, epoch);
 }
 
 } // namespace va
