@@ -8,11 +8,11 @@
 // A work-group walks its split in rounds of up to RT work-group tiles. Each
 // round first streams the K rows of its positions (with the K scales): every
 // row's raw score (q.k times the group scale) for each of the QG query heads
-// goes to the wave's slice of LDS and the wave keeps each head's maximum. Then it streams the V rows of the same
-// positions (with the V scales): each lane reads back its row's score and
-// accumulates p = exp2(score * qs - m) against the row, m being the exact
-// maximum of the wave's scores so far (one rescale of l and o per round, where
-// it rises). Reference: src/voltattn.cu:364-649 (one pass over the position
+// goes to the wave's slice of LDS, and the wave keeps each head's maximum. Then
+// it streams the V rows of the same positions (with the V scales): each lane
+// reads back its row's scores and accumulates p = exp2(score * qs - m) against
+// the row, m being the exact maximum of the wave's scores so far for that head
+// (one rescale of l and o per round, where it rises). Reference: src/voltattn.cu:364-649 (one pass over the position
 // that reads K and V together, an online softmax per position).
 //
 // Why two phases: a work-group that reads one stream at a time keeps half as
@@ -25,7 +25,8 @@
 //
 // Each lane loads LB = 16 bytes (12 for q3) of a row per load, U loads per
 // tile of one tensor; the loads of a 4-wave group interleave by instruction
-// (load u of wave w reads rows u*PPW*WAVES + w*PPW ..), as in decode_tiled.
+// (load u of wave w reads rows u*PPW*WAVES + w*PPW ..), as in decode_tiled,
+// and an 8-wave group keeps each wave's TW rows together.
 // Two register stages alternate over the stage sequence K tiles 0..T-1, V
 // tiles 0..T-1 of round 0, then round 1, ...: the next stage's loads are in
 // flight while the current one is computed, across the phase change too.
@@ -36,8 +37,8 @@
 
 namespace va {
 
-// Positions per round of a work-group: 32 KB of scores in LDS per query slot
-// at QG = 1, the same 32 KB split over the slots at QG > 1.
+// Positions per round of a work-group at QG = 1 (32 KB of scores in LDS); a
+// round at QG > 1 holds 8192/QG positions, so its scores take the same 32 KB.
 constexpr int PHASED_ROUND_ROWS = 8192;
 
 template <int KIND, int D, int G, int U, int WAVES, int QG = 1>
