@@ -12,8 +12,9 @@
 // it streams the V rows of the same positions (with the V scales): each lane
 // reads back its row's scores and accumulates p = exp2(score * qs - m) against
 // the row, m being the exact maximum of the wave's scores so far for that head
-// (one rescale of l and o per round, where it rises). Reference: src/voltattn.cu:364-649 (one pass over the position
-// that reads K and V together, an online softmax per position).
+// (one rescale of l and o per round, where it rises). Reference:
+// src/voltattn.cu:364-649 (one pass over the positions that reads K and V
+// together, an online softmax per position).
 //
 // Why two phases: a work-group that reads one stream at a time keeps half as
 // many DRAM streams open as one that reads K and V side by side. A read-only
