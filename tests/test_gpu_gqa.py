@@ -127,3 +127,16 @@ def test_gqa_equal_heads_is_va_decode():
             for x in bufs + [out, ws]:
                 x.free()
     np.testing.assert_array_equal(outs[0], outs[1])
+
+
+# Grouped f16+ runs the two-phase kernel (va_phased.hpp), whose rounds hold
+# 8192 / QG positions: splits of several rounds with a ragged last one, at four
+# query slots (Hq 8 / Hkv 2), two (Hq 4 / Hkv 2) and a group of three with one
+# masked slot (Hq 6 / Hkv 2).
+@pytest.mark.parametrize("shape", [(8, 2, 20000, 2), (4, 2, 9000, 1), (6, 2, 7000, 1)],
+                         ids=lambda s: "Hq{}-Hkv{}-L{}-S{}".format(*s))
+def test_gqa_f16_multi_round(shape):
+    Hq, Hkv, L, S = shape
+    print(f"gqa f16+ rounds Hq={Hq} Hkv={Hkv} L={L} S={S}", flush=True)
+    got, ref = _run(va.Fmt.F16M, Hq, Hkv, L, 128, 32, S, 0x7A0 + L)
+    _check(got, ref, ("f16+ rounds", Hq, Hkv, L, S))
