@@ -87,22 +87,29 @@ def test_paged_many_sequences_two_pass():
         _check(got[b].ravel(), pb.ref[b].ravel(), b)
 
 
+# (format, Hq, Hkv, page rows): the grouped-query kernels, and one query slot per
+# KV head with pages that hold a whole work-group tile of the two-phase kernel
+BAD_INPUT_CASES = [(va.Fmt.Q8M, 8, 2, 64), (va.Fmt.Q8M, 2, 2, 128), (va.Fmt.F16M, 2, 2, 64)]
+
+
+@pytest.mark.parametrize("case", BAD_INPUT_CASES, ids=lambda c: f"{c[0].label}-Hq{c[1]}-Hkv{c[2]}-P{c[3]}")
 @pytest.mark.parametrize("S", [0, 80])              # 0: fused merge; 80 > 64: the merge kernel
-def test_paged_empty_bad_page_and_overlong_sequence(S):
+def test_paged_empty_bad_page_and_overlong_sequence(S, case):
     """Length 0 -> zeros; a page id outside the pool, a length above
     max_seq_len or a negative length -> NaN for that sequence only; the others
     stay exact. Both merge paths (in the decode kernel and the separate
     lse_merge pass) give the same verdicts."""
+    fmt, Hq, Hkv, P = case
     lens = [300, 0, 300, 300, 0]
-    pb = batch_util.PagedBatch(va.Fmt.Q8M, lens, 8, 2, 128, 32, 64, seed=5, max_seq_len=320,
-                               max_pages=6)
+    pb = batch_util.PagedBatch(fmt, lens, Hq, Hkv, 128, 32, P, seed=5, max_seq_len=320,
+                               max_pages=384 // P)
     try:
         table = pb.table.copy()
         table[2, 1] = pb.shape.num_pages + 5          # sequence 2: second page id outside the pool
         seq = pb.seq_lens.copy()
         seq[3] = 321                                  # sequence 3: above max_seq_len
         seq[4] = -5                                   # sequence 4: negative length
-        print(f"paged bad inputs S={S}", flush=True)
+        print(f"paged bad inputs S={S} {fmt.label} Hq={Hq} Hkv={Hkv} P={P}", flush=True)
         got = pb.run(S=S, table=table, seq_lens=seq)
     finally:
         pb.free()

@@ -91,6 +91,11 @@ __device__ __forceinline__ void wait_all_mem() { __builtin_amdgcn_s_waitcnt(0); 
 
 // ------------------------------------------------------------------ scalars --
 __device__ __forceinline__ int uniform(int x) { return __builtin_amdgcn_readfirstlane(x); }
+__device__ __forceinline__ size_t uniform64(size_t x) {
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)x);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(x >> 32));
+    return ((size_t)hi << 32) | lo;
+}
 __device__ __forceinline__ float uniformf(float x) {
     return __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, x)));
 }

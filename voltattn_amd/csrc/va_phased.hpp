@@ -1,9 +1,12 @@
-// va_phased.hpp — the two-phase split-L decode kernel over contiguous K/V:
+// va_phased.hpp — the two-phase split-L decode kernel: over contiguous K/V,
 // the reference shape (one query head per K/V head, QG = 1) and grouped-query
-// decode of one sequence (QG query heads of a K/V head per work-group). The
-// same partials, splits, codecs and merge as decode_tiled<..., QG, PAGED =
-// false> (va_tiled.hpp), with the K and V rows of a split read in separate
-// phases.
+// decode of one sequence (QG query heads of a K/V head per work-group); over a
+// paged batch (PAGED), one query head per work-group. The same partials,
+// splits, codecs and merge as decode_tiled<..., QG, PAGED> (va_tiled.hpp), with
+// the K and V rows of a split read in separate phases. The paged form needs
+// pages of at least one work-group tile (TB rows, a power of two) and splits
+// that start on a tile, so that every tile lies in one page; the host checks
+// both.
 //
 // A work-group walks its split in rounds of up to RT work-group tiles. Each
 // round first streams the K rows of its positions (with the K scales): every
@@ -42,7 +45,7 @@ namespace va {
 // round at QG > 1 holds 8192/QG positions, so its scores take the same 32 KB.
 constexpr int PHASED_ROUND_ROWS = 8192;
 
-template <int KIND, int D, int G, int U, int WAVES, int QG = 1>
+template <int KIND, int D, int G, int U, int WAVES, int QG = 1, bool PAGED = false>
 __global__ __launch_bounds__(WAVES * 64, 1) void decode_phased(
     const uint8_t* k, const uint8_t* v, const uint16_t* sk, const uint16_t* sv,
     int L_, int S_, int chunk_, int slot_, const uint16_t* q, void* dst, DecodeArgs rest) {
@@ -72,16 +75,26 @@ __global__ __launch_bounds__(WAVES * 64, 1) void decode_phased(
     constexpr int SPG = NG >= 2 ? PPW * NG / 2 : PPW;  // scale entries of one load's rows
     static_assert(!QUANT || G % EPL == 0, "a lane's elements share one scale group");
     static_assert(SCE % 64 == 0 || SCR == 1, "scale entries fill whole wave loads");
+    static_assert(!PAGED || QG == 1, "the paged form carries one query slot");
+    static_assert(!PAGED || (TB & (TB - 1)) == 0, "paged tiles must not straddle pages");
 
     __shared__ uint32_t s_sc[WAVES][SCN];        // scale entries of the wave's current tile (low halves)
     __shared__ float s_score[WAVES][QG][RT * TW];  // raw scores of the wave's rows in the round
+    __shared__ int s_page[PAGED ? MAX_SPLIT_PAGES : 1];
 
     // work-group -> (KV head hk, query sub-group, split s)
     Route rt;
     rt.mg  = (int)blockIdx.x / a.S;
     rt.s   = (int)blockIdx.x - rt.mg * a.S;
-    int hk = rt.mg;
-    if constexpr (QG == 1) {                     // the reference's shape: head = merge group
+    int hk = rt.mg, b = 0;
+    if constexpr (PAGED) {                       // sequence b, KV head hk, one query head
+        const int sub = rt.mg % a.nsub;
+        const int r   = rt.mg / a.nsub;
+        hk = r % a.hkv;
+        b  = r / a.hkv;
+        rt.nq  = 1;
+        rt.oh0 = (b * a.hkv + hk) * a.qgroup + sub;
+    } else if constexpr (QG == 1) {              // the reference's shape: head = merge group
         rt.nq  = 1;
         rt.oh0 = rt.mg;
     } else {                                     // one sequence: merge group = (hk, sub-group)
@@ -98,8 +111,15 @@ __global__ __launch_bounds__(WAVES * 64, 1) void decode_phased(
     const int pw   = lane / LP;                  // row slot within a wave load
     const int grp  = (sl * EPL) / G;             // scale group of this lane
 
+    int L = a.L;
+    bool bad = false;                            // invalid input: the output becomes NaN
+    if constexpr (PAGED) {
+        const int cap = min(a.L, min(a.S * a.chunk, a.max_pages << a.page_shift));
+        L = a.seq_lens[b];
+        if (L > cap || L < 0) { bad = true; L = L < 0 ? 0 : cap; }   // outside [0, max_seq_len]: NaN output
+    }
     const int j0 = s * a.chunk;
-    const int n  = min(a.L - j0, a.chunk);       // rows of this split (<= 0: empty)
+    const int n  = min(L - j0, a.chunk);         // rows of this split (<= 0: empty)
 
     float m[QG], l[QG];
     float o[QG][EPL];
@@ -115,11 +135,25 @@ __global__ __launch_bounds__(WAVES * 64, 1) void decode_phased(
         const uint32_t lane_off = (uint32_t)(pw * ROWB + sl * LB);
         const int ntile = (n + TB - 1) / TB;     // work-group tiles of the split
         const int nst   = 2 * ntile;             // stages: a K and a V pass over every tile
-        const size_t row0 = (size_t)hk * a.L + j0;
-        const __amdgpu_buffer_rsrc_t rk = make_rsrc(a.k + row0 * ROWB, (uint32_t)n * ROWB);
-        const __amdgpu_buffer_rsrc_t rv = make_rsrc(a.v + row0 * ROWB, (uint32_t)n * ROWB);
-        const __amdgpu_buffer_rsrc_t rsk = QUANT ? make_rsrc(a.sk + row0 * NG, (uint32_t)n * NG * 2) : rk;
-        const __amdgpu_buffer_rsrc_t rsv = QUANT ? make_rsrc(a.sv + row0 * NG, (uint32_t)n * NG * 2) : rv;
+        // Contiguous form: resources over the split, tile offsets in soffset. The
+        // paged form builds resources per work-group tile (each lies in one
+        // page: the host launches it only for pages of at least TB rows and
+        // splits that start on a work-group tile).
+        const size_t   row0  = PAGED ? 0 : (size_t)hk * a.L + j0;
+        const uint32_t nsplt = PAGED ? 0u : (uint32_t)n;
+        const __amdgpu_buffer_rsrc_t rk = make_rsrc(a.k + row0 * ROWB, nsplt * ROWB);
+        const __amdgpu_buffer_rsrc_t rv = make_rsrc(a.v + row0 * ROWB, nsplt * ROWB);
+        const __amdgpu_buffer_rsrc_t rsk = QUANT ? make_rsrc(a.sk + row0 * NG, nsplt * NG * 2) : rk;
+        const __amdgpu_buffer_rsrc_t rsv = QUANT ? make_rsrc(a.sv + row0 * NG, nsplt * NG * 2) : rv;
+        int p0 = 0;
+        if constexpr (PAGED) {
+            // Stage the split's page ids (its positions span pages p0 .. p1).
+            p0 = j0 >> a.page_shift;
+            const int np = ((j0 + n - 1) >> a.page_shift) - p0 + 1;
+            const int32_t* tab = a.block_table + (size_t)b * a.max_pages + p0;
+            for (int i = (int)threadIdx.x; i < np; i += WAVES * 64) s_page[i] = tab[i];
+            __syncthreads();
+        }
 
         // Stage i -> (tile of the split, phase, tile within the round). Rounds
         // before the last hold RT tiles.
@@ -142,9 +176,25 @@ __global__ __launch_bounds__(WAVES * 64, 1) void decode_phased(
         // wait stays partial.
         auto load_stage = [&](int i, LoadT* xx, uint32_t* ss) {
             const StageAt st = stage_at(i);
-            const __amdgpu_buffer_rsrc_t tx = st.vph ? rv : rk;
-            const __amdgpu_buffer_rsrc_t ts = st.vph ? rsv : rsk;
-            const uint32_t t0 = (uint32_t)(st.tile * TB + wave * WS);
+            __amdgpu_buffer_rsrc_t tx = st.vph ? rv : rk;
+            __amdgpu_buffer_rsrc_t ts = st.vph ? rsv : rsk;
+            uint32_t t0 = (uint32_t)(st.tile * TB + wave * WS);
+            if constexpr (PAGED) {
+                // the work-group tile's rows in its page, every descriptor field
+                // scalar (a field in a VGPR would make each load a loop over lanes)
+                const int wt   = st.tile * TB;                      // tile's first row in the split
+                const int pos  = j0 + wt;                           // position in the sequence
+                const int rows = min(TB, n - wt);                   // >= 1: the tile is inside the split
+                const int page = uniform(s_page[(pos >> a.page_shift) - p0]);
+                const bool ok  = page >= 0 && page < a.num_pages;
+                bad = bad || !ok;
+                const uint32_t nrow = sgpr(ok ? (uint32_t)rows : 0u);
+                const size_t row = uniform64(((size_t)(ok ? page : 0) * a.hkv + hk) * ((size_t)1 << a.page_shift) +
+                                             (size_t)(pos & ((1 << a.page_shift) - 1)));
+                tx = make_rsrc((st.vph ? a.v : a.k) + row * ROWB, nrow * ROWB);
+                if constexpr (QUANT) ts = make_rsrc((st.vph ? a.sv : a.sk) + row * NG, nrow * NG * 2);
+                t0 = (uint32_t)(wave * WS);
+            }
             const uint32_t tpos = sgpr(t0);
             __builtin_amdgcn_sched_barrier(0);
             if constexpr (QUANT) {               // lanes past SCE repeat the last entry (unused)
@@ -311,7 +361,7 @@ __global__ __launch_bounds__(WAVES * 64, 1) void decode_phased(
         for (int q = 0; q < QG; ++q) fix_finish<C>(o[q], vsum[q], std::make_integer_sequence<int, EPL>{});
     }
 
-    group_finish<D, LP, EPL, WAVES, QG, false>(a, rt, m, l, o, false, epoch);
+    group_finish<D, LP, EPL, WAVES, QG, PAGED>(a, rt, m, l, o, bad, epoch);
 }
 
 } // namespace va
