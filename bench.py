@@ -586,7 +586,8 @@ def main() -> int:
                  ("paged", "q8+", dict(B=8, Hq=32, Hkv=8, L=16384, P=256)),
                  ("paged", "q4+", dict(B=8, Hq=32, Hkv=8, L=16384, P=256)),
                  ("paged", "q3+", dict(B=8, Hq=32, Hkv=8, L=16384, P=256)),
-                 ("paged", "q8+", dict(B=1, Hq=32, Hkv=32, L=16384, P=256))]
+                 ("paged", "q8+", dict(B=1, Hq=32, Hkv=32, L=16384, P=256)),
+                 ("paged", "f16+", dict(B=1, Hq=32, Hkv=32, L=16384, P=256))]
         for kind, name, p in specs:
             fmt = va.Fmt.parse(name)
             if kind == "gqa":
