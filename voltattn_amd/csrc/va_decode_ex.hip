@@ -144,20 +144,23 @@ int tile_positions_ex(int kind, int D) {
 #define VA_EX_PH_U 4
 #endif
 
-// Paged f16 with one query slot per KV head: the two-phase kernel's paged form
-// (4 waves, U = 4) when a page holds a whole work-group tile and splits start
-// on one; other page sizes stay on decode_tiled. Interleaved A/B on MI355X, B 1,
-// Hq = Hkv = 32, D 128, L 16384, against decode_tiled: pages of 256 42.60 ->
-// 40.67 us, pages of 64 43.59 -> 41.03. q8 stays on decode_tiled (16384 25.45
-// -> 25.33, 4096 10.17 -> 10.37).
+// Paged f16 and q8 with one query slot per KV head: the two-phase kernel's
+// paged form (4 waves, U = 4) when a page holds a whole work-group tile and
+// splits start on one; other page sizes stay on decode_tiled. Interleaved A/B on
+// MI355X, B 1, Hq = Hkv = 32, D 128, L 16384, against decode_tiled: f16 pages of
+// 256 42.60 -> 40.67 us, pages of 64 43.59 -> 41.03; q8 pages of 256 25.46 ->
+// 24.58 (page ids read a stage ahead), 4096 10.18 -> 10.21.
 #ifndef VA_EX_PHASED_PAGED
 #define VA_EX_PHASED_PAGED 1
+#endif
+#ifndef VA_EX_PHASED_PAGED_Q8
+#define VA_EX_PHASED_PAGED_Q8 1
 #endif
 
 template <int KIND, int D, int G, int QG, bool PAGED>
 static hipError_t launch_ex(int groups, const DecodeArgs& a, hipStream_t st) {
     constexpr int PTB = Tile<KIND, D>::PPW * 4 * 4;   // the paged form's work-group tile (a power of two)
-    if constexpr (VA_EX_PHASED_PAGED && QG == 1 && PAGED && KIND == KF16) {
+    if constexpr (VA_EX_PHASED_PAGED && QG == 1 && PAGED && (KIND == KF16 || (VA_EX_PHASED_PAGED_Q8 && KIND == KQ8))) {
         if ((1 << a.page_shift) >= PTB && a.chunk % PTB == 0) {
             hipLaunchKernelGGL((decode_phased<KIND, D, G, 4, 4, 1, true>), dim3((unsigned)(groups * a.S)), dim3(256),
                                0, st, VA_TILED_ARGS(a));

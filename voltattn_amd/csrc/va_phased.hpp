@@ -146,6 +146,7 @@ __global__ __launch_bounds__(WAVES * 64, 1) void decode_phased(
         const __amdgpu_buffer_rsrc_t rsk = QUANT ? make_rsrc(a.sk + row0 * NG, nsplt * NG * 2) : rk;
         const __amdgpu_buffer_rsrc_t rsv = QUANT ? make_rsrc(a.sv + row0 * NG, nsplt * NG * 2) : rv;
         int p0 = 0;
+        int pnext = 0;                           // page id of the next stage to load (paged form)
         if constexpr (PAGED) {
             // Stage the split's page ids (its positions span pages p0 .. p1).
             p0 = j0 >> a.page_shift;
@@ -153,6 +154,7 @@ __global__ __launch_bounds__(WAVES * 64, 1) void decode_phased(
             const int32_t* tab = a.block_table + (size_t)b * a.max_pages + p0;
             for (int i = (int)threadIdx.x; i < np; i += WAVES * 64) s_page[i] = tab[i];
             __syncthreads();
+            pnext = s_page[0];                   // stage 0: the split's first tile
         }
 
         // Stage i -> (tile of the split, phase, tile within the round). Rounds
@@ -185,7 +187,9 @@ __global__ __launch_bounds__(WAVES * 64, 1) void decode_phased(
                 const int wt   = st.tile * TB;                      // tile's first row in the split
                 const int pos  = j0 + wt;                           // position in the sequence
                 const int rows = min(TB, n - wt);                   // >= 1: the tile is inside the split
-                const int page = uniform(s_page[(pos >> a.page_shift) - p0]);
+                // quantized kinds (two resources per stage) take the page id read
+                // one stage ahead; f16 reads it here (measured faster for each)
+                const int page = QUANT ? uniform(pnext) : uniform(s_page[(pos >> a.page_shift) - p0]);
                 const bool ok  = page >= 0 && page < a.num_pages;
                 bad = bad || !ok;
                 const uint32_t nrow = sgpr(ok ? (uint32_t)rows : 0u);
@@ -209,6 +213,11 @@ __global__ __launch_bounds__(WAVES * 64, 1) void decode_phased(
 #pragma unroll
             for (int u = 0; u < U; ++u)
                 xx[u] = lane_load<KIND>(tx, lane_off + (uint32_t)(u * RS * ROWB), tpos * ROWB);
+            if constexpr (PAGED && QUANT) {
+                // the next stage's page id, read now so that it has arrived by its issue
+                const int in = min(i + 1, nst - 1);
+                pnext = s_page[((j0 + stage_at(in).tile * TB) >> a.page_shift) - p0];
+            }
             __builtin_amdgcn_sched_barrier(0);
         };
 
